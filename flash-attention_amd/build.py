@@ -1,0 +1,130 @@
+"""Builds the MI355X FlashAttention-2 forward in-tree.
+
+Outputs (next to the Python package, so they travel with the repository):
+  flash_attention_runtime/libfa_mi355x.so   HIP kernels + C ABI (hipcc, gfx950)
+  flash_attention_runtime/_C<EXT_SUFFIX>     torch/pybind binding over the C ABI
+
+Replaces the reference's JIT build (python/flash_attention_runtime/
+__init__.py:10-27, torch.utils.cpp_extension.load of _ext.cu with nvcc) by an
+explicit ahead-of-time build: one HIP code path for gfx950, no CUDA headers.
+
+Usage: python flash-attention_amd/build.py [--jobs N]
+"""
+from __future__ import annotations
+
+import argparse
+import os
+import shutil
+import subprocess
+import sys
+import sysconfig
+from concurrent.futures import ThreadPoolExecutor
+
+PKG_ROOT = os.path.dirname(os.path.abspath(__file__))
+REPO_ROOT = os.path.dirname(PKG_ROOT)
+CSRC = os.path.join(PKG_ROOT, "csrc")
+OUT_DIR = os.path.join(PKG_ROOT, "flash_attention_runtime")
+INCLUDE = os.path.join(REPO_ROOT, "include")
+BUILD_DIR = os.path.join(PKG_ROOT, "_build")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+
+ARCH = "gfx950"
+# -packed-fp32-ops: keep the compiler from forming v_pk_{add,mul,fma}_f32.
+HIP_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-Wall",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+
+
+def _run(cmd: list[str]) -> None:
+    proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    out = "\n".join(
+        ln for ln in proc.stdout.splitlines()
+        if "packed-fp32-ops" not in ln and "hip-link" not in ln
+        and "not a recognized feature for this target" not in ln
+    )
+    if proc.returncode != 0:
+        sys.stderr.write(out + "\n")
+        raise RuntimeError(f"build step failed ({proc.returncode}): {' '.join(cmd)}")
+
+
+def _hipcc() -> str:
+    for cand in (os.path.join(ROCM, "bin", "hipcc"), shutil.which("hipcc")):
+        if cand and os.path.exists(cand):
+            return cand
+    raise RuntimeError("hipcc not found")
+
+
+def build_hip_library(jobs: int) -> str:
+    """Compiles every csrc/*.hip and fa_api.cpp with hipcc and links the
+    shared library libfa_mi355x.so."""
+    os.makedirs(BUILD_DIR, exist_ok=True)
+    hipcc = _hipcc()
+    sources = [
+        os.path.join(CSRC, "fa_fwd_kernel.hip"),
+        os.path.join(CSRC, "fa_api.cpp"),
+    ]
+    objs = []
+    cmds = []
+    for src in sources:
+        obj = os.path.join(BUILD_DIR, os.path.basename(src) + ".o")
+        objs.append(obj)
+        lang = ["-x", "hip"] if src.endswith(".hip") else []
+        cmds.append([hipcc, *HIP_FLAGS, "-I", INCLUDE, "-I", CSRC, *lang, "-c", src, "-o", obj])
+    with ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
+        list(ex.map(_run, cmds))
+    lib = os.path.join(OUT_DIR, "libfa_mi355x.so")
+    tmp = lib + ".tmp"
+    _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp])
+    os.replace(tmp, lib)
+    return lib
+
+
+def build_torch_binding() -> str:
+    """Compiles the pybind/torch host binding (fa_torch_ext.cpp) with g++ and
+    links it against libfa_mi355x.so (rpath $ORIGIN)."""
+    import torch
+    from torch.utils import cpp_extension
+
+    torch_lib = os.path.join(os.path.dirname(torch.__file__), "lib")
+    ext_suffix = sysconfig.get_config_var("EXT_SUFFIX") or ".so"
+    out = os.path.join(OUT_DIR, "_C" + ext_suffix)
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    incs = [*cpp_extension.include_paths(), sysconfig.get_paths()["include"],
+            os.path.join(ROCM, "include"), INCLUDE]
+    cmd = [
+        "g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-w",
+        "-DTORCH_EXTENSION_NAME=_C", "-DTORCH_API_INCLUDE_EXTENSION_H",
+        f"-D_GLIBCXX_USE_CXX11_ABI={abi}", "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1",
+        *[f"-I{p}" for p in incs],
+        os.path.join(CSRC, "fa_torch_ext.cpp"),
+        f"-L{OUT_DIR}", "-lfa_mi355x",
+        f"-L{torch_lib}", "-lc10", "-ltorch", "-ltorch_cpu", "-ltorch_python", "-lc10_hip",
+        "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{torch_lib}",
+        "-o", out + ".tmp",
+    ]
+    _run(cmd)
+    os.replace(out + ".tmp", out)
+    return out
+
+
+def build(jobs: int = 8) -> list[str]:
+    lib = build_hip_library(jobs)
+    ext = build_torch_binding()
+    return [lib, ext]
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--jobs", type=int, default=8)
+    args = ap.parse_args()
+    for path in build(args.jobs):
+        print("built", os.path.relpath(path, REPO_ROOT))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,447 @@
+// FlashAttention-2 forward for MI355X (gfx950 / CDNA4).
+//
+// Replaces the reference kernel flash_attention_forward_v6_mma
+// (src/forward/forward_v6_mma.cuh:325-412) and its building blocks
+// (src/loadstore, src/tensor_core, src/softmax, src/ptx).  It is written for
+// the CDNA4 execution model rather than translated from the mma.sync design:
+//
+//  * One workgroup = NW wave64s, each wave owns 32 query rows (BM = 32*NW).
+//  * S^T = K * Q^T on v_mfma_f32_32x32x16_{f16,bf16}: K tile rows are the A
+//    operand (read from LDS), Q rows are the B operand (kept in VGPRs for the
+//    whole kernel).  In the 32x32 accumulator layout lane l holds column
+//    l%32 — one query row — and 16 keys, so the online-softmax row max and row
+//    sum are in-lane; only lanes l and l^32 share a row (one cross-half swap).
+//  * O^T += V^T * P^T on the same MFMA.  P^T is taken straight from the S^T
+//    accumulator registers as the B operand: the MFMA contraction index is
+//    mapped to keys by a fixed permutation sigma (k-slot 8g+t of lane group g
+//    <-> key 8*(t/4) + 4g + t%4 inside each 16-key chunk), and the V^T A
+//    operand is fetched with the same sigma using ds_read_b64_tr_b16, the
+//    gfx950 transposing LDS read, so no register shuffle is needed.
+//  * K and V tiles (64 keys) are staged by global_load_lds_dwordx4 (direct
+//    global->LDS, 16 B per lane, no VGPR round trip) into a double-buffered
+//    LDS ring; the loads of tile t+1 fly while tile t is computed.  Each tile
+//    carries an XOR swizzle on its 16-byte chunks chosen so the K reads
+//    (ds_read_b128) and the V transposed reads hit distinct banks.
+//  * Causal: fully-masked K tiles are never loaded or computed; q-tiles are
+//    dispatched longest-first.  Ragged N: loads clamp to the last row and the
+//    scores of keys >= N are -inf; rows >= N are never stored.
+//  * Block ids are remapped so each XCD (private L2) works on consecutive
+//    q-tiles of the same heads.
+//
+// Numerics follow the reference (src/softmax/online_softmax.cuh:13-19,
+// :89-152; src/forward/forward_v6_mma.cuh:19-38): fp32 scores, running max m
+// of the raw scores, p = exp2(s*c - m*c) with c = scale*log2(e), O and l
+// rescaled by exp2((m_old - m_new)*c), P rounded to the input type with
+// round-to-nearest-even before the PV product, l summed from the unrounded
+// fp32 p, O normalised in fp32 and rounded to the input type.  New relative to
+// the reference: the natural-log LSE = m*scale + ln(l).
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <type_traits>
+
+#include "fa_fwd_kernel.h"
+
+namespace fa {
+namespace {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef short i16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4_t;
+typedef __attribute__((address_space(3))) i16x8 lds_i16x8_t;
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kNumXcd = 8;  // MI355X: 8 XCDs, blocks dispatched round-robin
+
+template <bool BF16>
+struct ElemOps;
+
+template <>
+struct ElemOps<false> {
+  using scalar = _Float16;
+  static __device__ __forceinline__ f32x16 mfma(i16x8 a, i16x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                 __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+};
+
+template <>
+struct ElemOps<true> {
+  using scalar = __bf16;
+  static __device__ __forceinline__ f32x16 mfma(i16x8 a, i16x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                  __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+};
+
+// Two fp32 -> packed pair of the element type, round-to-nearest-even.
+template <bool BF16>
+__device__ __forceinline__ uint32_t pack2(float x, float y) {
+  using S = typename ElemOps<BF16>::scalar;
+  S a = static_cast<S>(x);
+  S b = static_cast<S>(y);
+  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, a)) |
+         (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, b)) << 16);
+}
+
+// Compile-time loop: f(std::integral_constant<int, I>) for I in [B, E).
+template <int B, int E, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Value of lane (l ^ 32) for every lane l.
+__device__ __forceinline__ float swap_halves(float x) {
+  return __shfl_xor(x, 32, 64);
+}
+
+// Hardware dispatches workgroup b to XCD b % 8.  Map the dispatch order to a
+// logical order in which XCD x owns the contiguous logical range
+// [start_x, start_x + count_x), so the blocks that share a head's K/V run on
+// the same L2.  Bijective for any total.
+__device__ __forceinline__ int xcd_remap(int b, int total) {
+  const int per = (total + kNumXcd - 1) / kNumXcd;
+  int tall = total % kNumXcd;
+  if (tall == 0) tall = kNumXcd;
+  const int xcd = b % kNumXcd;
+  const int local = b / kNumXcd;
+  if (xcd < tall) return xcd * per + local;
+  return tall * per + (xcd - tall) * (per - 1) + local;
+}
+
+template <int D>
+struct Tile {
+  static constexpr int BN = 64;                 // keys per K/V tile
+  static constexpr int ROWB = D * 2;            // bytes per K/V row
+  static constexpr int BYTES = BN * ROWB;       // bytes per K or V tile
+  static constexpr int CHUNKS = ROWB / 16;      // 16-byte chunks per row
+  // K tile: the 32x32x16 A-operand read is ds_read_b128 of one 16-byte chunk
+  // per lane for 32 consecutive keys; XOR the chunk index with key bits so
+  // consecutive keys land on distinct bank groups.
+  static __device__ __forceinline__ int swz_k(int key) {
+    return D == 128 ? (key & 15) : ((key >> 1) & 7);
+  }
+  // V tile: a transposed read covers 4 consecutive keys x 64 contiguous bytes
+  // per half-wave; XOR the 64-byte segment so the 4 keys hit distinct banks.
+  static __device__ __forceinline__ int swz_v(int key) {
+    return D == 128 ? ((key & 3) << 2) : (((key >> 1) & 1) << 2);
+  }
+};
+
+// 32-bit LDS address of a pointer into __shared__ memory.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const lds_void_t*)(p);
+}
+
+// One global_load_lds_dwordx4: lane i copies 16 bytes from its own `src` to
+// LDS byte address lds_base + 16*i (lds_base is wave-uniform, passed in M0).
+// Issued from inline asm on purpose: the compiler cannot tell which LDS
+// bytes an in-flight DMA writes, so with the builtin it would put a full
+// vmcnt(0) wait in front of every later LDS read of the *other* buffer,
+// serialising the prefetch.  The kernel instead orders the DMA explicitly:
+// each tile ends with s_waitcnt vmcnt(0) followed by a workgroup barrier
+// before any wave reads the freshly written buffer.
+__device__ __forceinline__ void dma_16b(const void* src, const void* lds_dst_wave_base) {
+  const uint32_t base = __builtin_amdgcn_readfirstlane(lds_addr(lds_dst_wave_base));
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+               :
+               : "v"(src), "s"(base)
+               : "memory", "m0");
+}
+
+// Two ds_read_b64_tr_b16 (the gfx950 transposing LDS read) at byte
+// addresses addr+OFF0 and addr+OFF1, concatenated into one 8 x 16-bit MFMA
+// operand.  Within each 16-lane group, lane i receives element (i & 3) of
+// the 4 x 16-bit words addressed by lanes 4e + (i >> 2), e = 0..3.
+// Issued from inline asm so the compiler does not put a vmcnt(0) wait for the
+// in-flight K/V prefetch DMA in front of it; the lgkmcnt wait is chained
+// through the result registers so no consumer can be scheduled above it.
+template <int OFF0, int OFF1>
+__device__ __forceinline__ i16x8 ds_read_tr_pair(uint32_t addr) {
+  i16x4 lo, hi;
+  asm volatile("ds_read_b64_tr_b16 %0, %2 offset:%3\n\t"
+               "ds_read_b64_tr_b16 %1, %2 offset:%4"
+               : "=v"(lo), "=v"(hi)
+               : "v"(addr), "i"(OFF0), "i"(OFF1));
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(lo), "+v"(hi));
+  return i16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
+// Stage rows [row0, row0+64) of one head of K (or V) into an LDS tile with
+// global_load_lds_dwordx4.  Lane i of a wave instruction lands at
+// base + 16*i, so the swizzle is applied on the source side: the lane that
+// fills physical chunk pc of row r reads logical chunk pc ^ swz(r).
+template <int D, int NW, bool IS_V>
+__device__ __forceinline__ void stage_tile(const char* __restrict__ gbase, int64_t row_stride_b,
+                                           int row0, int n_rows, char* lds_tile, int wave,
+                                           int lane) {
+  using T = Tile<D>;
+  constexpr int ITERS = T::BYTES / (1024 * NW);
+  static_assert(ITERS >= 1 && T::BYTES % (1024 * NW) == 0, "tile must split evenly over waves");
+#pragma unroll
+  for (int it = 0; it < ITERS; ++it) {
+    const int inst = wave * ITERS + it;
+    const int off = inst * 1024 + lane * 16;
+    const int r = off / T::ROWB;
+    const int pc = (off % T::ROWB) / 16;
+    const int c = pc ^ (IS_V ? T::swz_v(r) : T::swz_k(r));
+    int grow = row0 + r;
+    grow = grow < n_rows ? grow : n_rows - 1;
+    const char* src = gbase + grow * row_stride_b + c * 16;
+    dma_16b(src, lds_tile + inst * 1024);
+  }
+}
+
+template <int D, bool BF16, bool CAUSAL, int NW>
+__global__ void __launch_bounds__(NW * 64)
+    fa_fwd_kernel(const KernelArgs args) {
+  using T = Tile<D>;
+  using Ops = ElemOps<BF16>;
+  constexpr int BM = 32 * NW;
+  constexpr int BN = T::BN;
+  constexpr int KSTEPS = D / 16;  // MFMA k-steps for S^T (k = head dim)
+  constexpr int DBLK = D / 32;    // 32-wide head-dim blocks of O^T
+
+  __shared__ __attribute__((aligned(1024))) char smem[4 * T::BYTES];
+  // LDS ring: K buffers 0/1 then V buffers 0/1.
+  auto k_lds = [&](int i) { return smem + i * T::BYTES; };
+  auto v_lds = [&](int i) { return smem + (2 + i) * T::BYTES; };
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int l32 = lane & 31;
+  const int g = lane >> 5;        // which half of the wave
+  const int lj = lane & 15;       // lane within its 16-lane group
+  const int hg = (lane >> 4) & 1; // 16-lane group within the half
+
+  const int N = args.seq_len;
+  const int logical = xcd_remap(blockIdx.x, gridDim.x);
+  const int bh = logical / args.n_qblocks;
+  int qb = logical - bh * args.n_qblocks;
+  if (CAUSAL) qb = args.n_qblocks - 1 - qb;  // longest q-tiles first
+  const int b = bh / args.heads;
+  const int h = bh - b * args.heads;
+
+  const char* __restrict__ qh = reinterpret_cast<const char*>(args.q) +
+                                2 * (b * args.q_stride_b + h * args.q_stride_h);
+  const char* __restrict__ kh = reinterpret_cast<const char*>(args.k) +
+                                2 * (b * args.k_stride_b + h * args.k_stride_h);
+  const char* __restrict__ vh = reinterpret_cast<const char*>(args.v) +
+                                2 * (b * args.v_stride_b + h * args.v_stride_h);
+  char* __restrict__ oh = reinterpret_cast<char*>(args.o) +
+                          2 * (b * args.o_stride_b + h * args.o_stride_h);
+  const int64_t qsb = 2 * args.q_stride_s, ksb = 2 * args.k_stride_s;
+  const int64_t vsb = 2 * args.v_stride_s, osb = 2 * args.o_stride_s;
+
+  const int q0 = qb * BM;
+  const int wrow0 = q0 + wave * 32;  // first query row of this wave
+  const int qrow = wrow0 + l32;      // this lane's query row
+  const int kv_end = CAUSAL ? min(N, q0 + BM) : N;
+  const int n_tiles = (kv_end + BN - 1) / BN;
+
+  // Start streaming tile 0 while Q is fetched into registers.
+  stage_tile<D, NW, false>(kh, ksb, 0, N, k_lds(0), wave, lane);
+  stage_tile<D, NW, true>(vh, vsb, 0, N, v_lds(0), wave, lane);
+
+  // Q as the B operand of S^T = K Q^T: lane holds query qrow, dims
+  // [16*kk + 8*g, +8) for k-step kk.
+  i16x8 qf[KSTEPS];
+  {
+    const int qr = qrow < N ? qrow : N - 1;
+    const char* qp = qh + qr * qsb + g * 16;
+#pragma unroll
+    for (int kk = 0; kk < KSTEPS; ++kk)
+      qf[kk] = *reinterpret_cast<const i16x8*>(qp + kk * 32);
+  }
+
+  f32x16 o_acc[DBLK];
+#pragma unroll
+  for (int db = 0; db < DBLK; ++db)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o_acc[db][i] = 0.0f;
+  float m_run = -INFINITY;  // running max of raw scores (this query row)
+  float l_run = 0.0f;       // this lane's partial sum of p
+  const float c = args.scale_log2;
+
+  // Per-lane LDS byte offsets inside a tile (loop invariant).
+  // K: A operand of key block kb, k-step kk -> row kb*32 + l32, chunk 2kk+g.
+  int k_off[KSTEPS];
+  {
+    const int key = l32;  // kb adds 32 rows = 32*ROWB bytes; swizzle uses key%16 or (key>>1)%8
+#pragma unroll
+    for (int kk = 0; kk < KSTEPS; ++kk)
+      k_off[kk] = key * T::ROWB + (((2 * kk + g) ^ T::swz_k(key)) << 4);
+  }
+  // V^T: transposed read for 16-key chunk ch, half hf, head-dim block db:
+  // this lane supplies row key = 16ch + 8hf + 4g + (lj>>2) and
+  // columns 32db + 16hg + 4(lj&3) .. +3.
+  int v_off[DBLK];
+  {
+    const int key = 4 * g + (lj >> 2);  // + 16ch + 8hf: multiples of 4 keep swz_v
+#pragma unroll
+    for (int db = 0; db < DBLK; ++db) {
+      const int col = 32 * db + 16 * hg + 4 * (lj & 3);
+      const int chunk = col >> 3;
+      v_off[db] = key * T::ROWB + ((chunk ^ T::swz_v(key)) << 4) + (col & 7) * 2;
+    }
+  }
+
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  for (int t = 0; t < n_tiles; ++t) {
+    const int buf = t & 1;
+    if (t + 1 < n_tiles) {
+      stage_tile<D, NW, false>(kh, ksb, (t + 1) * BN, N, k_lds(buf ^ 1), wave, lane);
+      stage_tile<D, NW, true>(vh, vsb, (t + 1) * BN, N, v_lds(buf ^ 1), wave, lane);
+    }
+    const int kt0 = t * BN;
+    // Skip tiles whose every key lies after every row of this wave.
+    const bool wave_active = !CAUSAL || kt0 <= wrow0 + 31;
+    if (wave_active) {
+      const char* kt = k_lds(buf);
+      const char* vt = v_lds(buf);
+
+      // ---- S^T = K Q^T : two 32-key blocks ----
+      f32x16 s[2];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) s[kb][i] = 0.0f;
+#pragma unroll
+        for (int kk = 0; kk < KSTEPS; ++kk) {
+          const i16x8 a = *reinterpret_cast<const i16x8*>(kt + kb * 32 * T::ROWB + k_off[kk]);
+          s[kb] = Ops::mfma(a, qf[kk], s[kb]);
+        }
+      }
+
+      // ---- masking (ragged tail / causal diagonal) ----
+      const bool need_mask = (kt0 + BN > N) || (CAUSAL && kt0 + BN - 1 > wrow0);
+      if (need_mask) {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int key = kt0 + kb * 32 + 8 * (i >> 2) + 4 * g + (i & 3);
+            const bool masked = key >= N || (CAUSAL && key > qrow);
+            if (masked) s[kb][i] = -INFINITY;
+          }
+      }
+
+      // ---- online softmax (reference online_softmax.cuh:89-152) ----
+      float mx = s[0][0];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[kb][i]);
+      mx = fmaxf(mx, swap_halves(mx));
+      const float m_new = fmaxf(m_run, mx);
+      const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+      const float alpha = fast_exp2((m_run - m_use) * c);
+      const float mc = m_use * c;
+      float rs = 0.0f;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const float p = fast_exp2(fmaf(s[kb][i], c, -mc));
+          s[kb][i] = p;
+          rs += p;
+        }
+      l_run = fmaf(l_run, alpha, rs);
+      m_run = m_new;
+#pragma unroll
+      for (int db = 0; db < DBLK; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o_acc[db][i] *= alpha;
+
+      // ---- P^T as B operand: chunk ch = 2kb + hh uses S regs 8hh..8hh+7 ----
+      i16x8 pf[4];
+#pragma unroll
+      for (int ch = 0; ch < 4; ++ch) {
+        const int kb = ch >> 1, base = (ch & 1) * 8;
+        uint32_t w0 = pack2<BF16>(s[kb][base + 0], s[kb][base + 1]);
+        uint32_t w1 = pack2<BF16>(s[kb][base + 2], s[kb][base + 3]);
+        uint32_t w2 = pack2<BF16>(s[kb][base + 4], s[kb][base + 5]);
+        uint32_t w3 = pack2<BF16>(s[kb][base + 6], s[kb][base + 7]);
+        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+        u32x4 w = {w0, w1, w2, w3};
+        pf[ch] = __builtin_bit_cast(i16x8, w);
+      }
+
+      // ---- O^T += V^T P^T ----
+#pragma unroll
+      for (int db = 0; db < DBLK; ++db) {
+        const uint32_t addr = lds_addr(vt + v_off[db]);
+        static_for<0, 4>([&](auto ch_c) {
+          constexpr int ch = decltype(ch_c)::value;
+          const i16x8 a = ds_read_tr_pair<ch * 16 * T::ROWB, ch * 16 * T::ROWB + 8 * T::ROWB>(addr);
+          o_acc[db] = Ops::mfma(a, pf[ch], o_acc[db]);
+        });
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+
+  // ---- epilogue: combine the two half-row partial sums, normalise, store ----
+  const float l_tot = l_run + swap_halves(l_run);
+  const bool row_ok = qrow < N;
+  const float inv_l = (row_ok && l_tot > 0.0f) ? 1.0f / l_tot : 0.0f;
+  if (row_ok) {
+    char* op = oh + qrow * osb;
+#pragma unroll
+    for (int db = 0; db < DBLK; ++db)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int col = 32 * db + 8 * r + 4 * g;
+        uint32_t w0 = pack2<BF16>(o_acc[db][4 * r + 0] * inv_l, o_acc[db][4 * r + 1] * inv_l);
+        uint32_t w1 = pack2<BF16>(o_acc[db][4 * r + 2] * inv_l, o_acc[db][4 * r + 3] * inv_l);
+        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+        u32x2 w = {w0, w1};
+        *reinterpret_cast<u32x2*>(op + col * 2) = w;
+      }
+    if (args.lse != nullptr && g == 0) {
+      const float m_use = m_run == -INFINITY ? 0.0f : m_run;
+      args.lse[(int64_t)bh * N + qrow] = m_use * args.scale + __logf(l_tot);
+    }
+  }
+}
+
+template <int D, bool BF16, bool CAUSAL, int NW>
+hipError_t launch_one(const KernelArgs& a, hipStream_t stream) {
+  constexpr int BM = 32 * NW;
+  KernelArgs args = a;
+  args.n_qblocks = (args.seq_len + BM - 1) / BM;
+  const int64_t total = (int64_t)args.n_qblocks * args.batch * args.heads;
+  if (total > 0x7fffffff) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((fa_fwd_kernel<D, BF16, CAUSAL, NW>), dim3((unsigned)total), dim3(NW * 64),
+                     0, stream, args);
+  return hipGetLastError();
+}
+
+template <int D, bool BF16>
+hipError_t launch_causal(const KernelArgs& a, hipStream_t stream) {
+  return a.causal ? launch_one<D, BF16, true, 4>(a, stream)
+                  : launch_one<D, BF16, false, 4>(a, stream);
+}
+
+}  // namespace
+
+hipError_t launch_fwd(const KernelArgs& a, hipStream_t stream) {
+  if (a.head_dim == 128)
+    return a.bf16 ? launch_causal<128, true>(a, stream) : launch_causal<128, false>(a, stream);
+  return a.bf16 ? launch_causal<64, true>(a, stream) : launch_causal<64, false>(a, stream);
+}
+
+}  // namespace fa

@@ -1,0 +1,126 @@
+/*
+ * fa_mi355x.h — C ABI of the MI355X (gfx950) FlashAttention-2 forward library.
+ *
+ * This is the drop-in boundary for the reference's forward path.  Every entry
+ * point takes plain pointers and sizes; no torch or HIP types appear in the
+ * signatures (a HIP stream is passed as `void*`, NULL meaning the null stream).
+ *
+ * Reference interfaces replaced (paths under the reference repository):
+ *   - fa_fwd          <- launch_fp16 + the kernel launch
+ *                        python/flash_attention_runtime/_ext.cu:59-122,
+ *                        and the kernel argument block ForwardKernelArgs
+ *                        src/config/config.cuh:20-45
+ *   - fa_fwd_validate <- validate_inputs / check_cuda_tensor
+ *                        python/flash_attention_runtime/_ext.cu:19-57
+ *   - fa_fwd_timed    <- fa_forward(..., benchmark=true) event timing
+ *                        python/flash_attention_runtime/_ext.cu:124-158
+ *   - fa_device_info  <- utils/get_gpu_hardware_param.cu:1-26 and the peak
+ *                        table infer_device_peak_specs
+ *                        benchmark/cpp/include/perf_metrics.cuh:78-120
+ *
+ * Semantics (all entry points):
+ *   O[b,h,i,:] = sum_j softmax_j(scale * Q[b,h,i,:].K[b,h,j,:] + mask_ij) V[b,h,j,:]
+ *   LSE[b,h,i] = ln sum_j exp(scale * Q[b,h,i,:].K[b,h,j,:] + mask_ij)   (natural log)
+ *   mask_ij = -inf when causal and j > i (top-left aligned), else 0.
+ * Tensors are [batch, heads, seq_len, head_dim] with unit stride along
+ * head_dim; the batch/head/seq strides are free (so BNHD views work without a
+ * copy).  O has the input dtype; LSE is fp32 [batch, heads, seq_len],
+ * contiguous, and optional.
+ *
+ * Ownership: all pointers are borrowed; the library allocates no device memory.
+ * Threading: re-entrant; the only mutable global state is a thread-local error
+ * string.  Streams: fa_fwd is asynchronous on `stream`; unlike the reference
+ * kernel, an unsupported argument never turns into a silent device no-op —
+ * it is rejected on the host with a status code before anything is launched.
+ */
+#ifndef FA_MI355X_H
+#define FA_MI355X_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+  FA_OK = 0,
+  FA_ERR_NULL = 1,        /* a required pointer is NULL                          */
+  FA_ERR_DTYPE = 2,       /* dtype is not FA_DTYPE_F16 / FA_DTYPE_BF16           */
+  FA_ERR_SHAPE = 3,       /* batch, heads or seq_len < 1                         */
+  FA_ERR_HEADDIM = 4,     /* head_dim not in {64, 128}                           */
+  FA_ERR_STRIDE = 5,      /* negative / misaligned stride or pointer             */
+  FA_ERR_UNSUPPORTED = 6, /* shape beyond the kernels' index range               */
+  FA_ERR_HIP = 7,         /* a HIP runtime call failed (see fa_last_error)       */
+  FA_ERR_ARG = 8          /* softmax_scale not finite and > 0, causal not 0/1    */
+} fa_status;
+
+typedef enum { FA_DTYPE_F16 = 0, FA_DTYPE_BF16 = 1 } fa_dtype;
+
+/* Kernel argument block.  Mirrors ForwardKernelArgs (src/config/config.cuh:20-45)
+ * with 64-bit strides, a dtype tag, the causal flag and an optional LSE output.
+ * Strides are in elements: [0] batch, [1] head, [2] seq.  head_dim stride is 1. */
+typedef struct {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o;
+  float* lse; /* may be NULL: then no logsumexp is written */
+  int64_t q_stride[3];
+  int64_t k_stride[3];
+  int64_t v_stride[3];
+  int64_t o_stride[3];
+  int32_t batch;
+  int32_t heads;
+  int32_t seq_len;
+  int32_t head_dim;
+  float softmax_scale; /* the reference passes 1/sqrt(head_dim) (_ext.cu:93) */
+  int32_t causal;      /* 0 or 1 */
+  int32_t dtype;       /* fa_dtype */
+} fa_fwd_params;
+
+/* Device description (replaces utils/get_gpu_hardware_param.cu:1-26). */
+typedef struct {
+  char name[256];
+  char arch[64];
+  int32_t compute_units;
+  int32_t clock_khz;
+  int64_t lds_per_cu_bytes;
+  int64_t l2_bytes;
+  int32_t memory_bus_width_bits;
+  int32_t memory_clock_khz;
+  /* compute_units x clock x 4096 dense fp16/bf16 MFMA flop per clock per CU */
+  double fp16_dense_peak_tflops;
+  /* 2 x bus width x memory clock (DDR) */
+  double hbm_peak_gbps;
+} fa_device_info_t;
+
+/* Host-only argument check; touches no GPU.  Returns FA_OK or the first
+ * failing rule (see fa_status).  Replaces _ext.cu:19-57. */
+fa_status fa_fwd_validate(const fa_fwd_params* p);
+
+/* Validate, then launch the forward kernel asynchronously on `stream`
+ * (a hipStream_t; NULL = null stream).  Replaces _ext.cu:59-122. */
+fa_status fa_fwd(const fa_fwd_params* p, void* stream);
+
+/* fa_fwd bracketed by two HIP events on `stream`; blocks until the kernel has
+ * finished and writes its elapsed time in milliseconds to *ms.
+ * Replaces the benchmark=true branch of fa_forward (_ext.cu:136-155). */
+fa_status fa_fwd_timed(const fa_fwd_params* p, void* stream, float* ms);
+
+/* Static description of a status code. */
+const char* fa_status_str(fa_status s);
+
+/* Detail of the last failure on the calling thread ("" if none). */
+const char* fa_last_error(void);
+
+/* Query device `device`.  Returns FA_OK, FA_ERR_NULL or FA_ERR_HIP. */
+fa_status fa_device_info(int device, fa_device_info_t* out);
+
+/* Library version string, e.g. "fa_mi355x 0.1.0 gfx950". */
+const char* fa_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FA_MI355X_H */

@@ -1,0 +1,108 @@
+"""Known-answer tests of the MFMA operand layouts and the transposing LDS read
+the forward kernel relies on (re-derived from the reference's MMA KATs,
+tests/unit/ptx/test_mma_fragment.cu and tests/unit/loadstore/test_copy_srm.cu,
+for v_mfma_f32_32x32x16 instead of mma.sync m16n8k16)."""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+@pytest.fixture(scope="module")
+def kat():
+    path = os.path.join(HERE, "kat", "libfa_kat.so")
+    L = ctypes.CDLL(path)
+    u16p = ctypes.POINTER(ctypes.c_uint16)
+    fp = ctypes.POINTER(ctypes.c_float)
+    L.kat_mfma_32x32x16.argtypes = [ctypes.c_int, u16p, u16p, fp, fp]
+    L.kat_ds_read_tr16.argtypes = [ctypes.POINTER(ctypes.c_int16)]
+    return L
+
+
+def _bits(x, bf16, oracle):
+    vals, bits = (oracle.round_bf16 if bf16 else oracle.round_f16)(np.asarray(x, np.float32))
+    return vals, bits
+
+
+def _run(kat, bf16, a_bits, b_bits, c):
+    a_bits = np.ascontiguousarray(a_bits, np.uint16)
+    b_bits = np.ascontiguousarray(b_bits, np.uint16)
+    c = np.ascontiguousarray(c, np.float32)
+    d = np.zeros((32, 32), np.float32)
+    u16p = ctypes.POINTER(ctypes.c_uint16)
+    fp = ctypes.POINTER(ctypes.c_float)
+    rc = kat.kat_mfma_32x32x16(int(bf16), a_bits.ctypes.data_as(u16p), b_bits.ctypes.data_as(u16p),
+                               c.ctypes.data_as(fp), d.ctypes.data_as(fp))
+    assert rc == 0, f"HIP error {rc}"
+    return d
+
+
+@pytest.mark.parametrize("bf16", [False, True], ids=["f16", "bf16"])
+def test_mfma_constant_kat(kat, oracle, bf16):
+    """A = 0.5, B = 0.25, C = 1.5 -> every D = 1.5 + K * 0.125 = 3.5 for K = 16
+    (the reference's constant case, test_mma_fragment.cu:184-213, also K = 16)."""
+    print(f"case mfma constant bf16={bf16}", flush=True)
+    _, a = _bits(np.full((32, 16), 0.5), bf16, oracle)
+    _, b = _bits(np.full((16, 32), 0.25), bf16, oracle)
+    d = _run(kat, bf16, a, b, np.full((32, 32), 1.5))
+    assert np.all(d == 3.5)
+
+
+@pytest.mark.parametrize("bf16", [False, True], ids=["f16", "bf16"])
+def test_mfma_pattern_kat(kat, oracle, bf16):
+    """Non-integer patterns of test_mma_fragment.cu:76-121 / :236-267:
+    A[m][k] = 0.10(m+1) + 0.01(k+1) + 0.003, B[k][n] = 0.07(k+1) - 0.015(n+1) + 0.004,
+    C = 0.123, compared with the fp32 sum of the quantised operands (tol 1e-2)."""
+    print(f"case mfma pattern bf16={bf16}", flush=True)
+    m = np.arange(32)[:, None]
+    k = np.arange(16)[None, :]
+    A = 0.10 * (m + 1) + 0.01 * (k + 1) + 0.003
+    kk = np.arange(16)[:, None]
+    n = np.arange(32)[None, :]
+    B = 0.07 * (kk + 1) - 0.015 * (n + 1) + 0.004
+    av, a = _bits(A, bf16, oracle)
+    bv, b = _bits(B, bf16, oracle)
+    d = _run(kat, bf16, a, b, np.full((32, 32), 0.123))
+    ref = av.astype(np.float64) @ bv.astype(np.float64) + 0.123
+    assert np.abs(d - ref).max() <= 1e-2
+    # Exactness of the layout: a transposed operand would be far off.
+    assert np.abs(d - ref).max() <= 1e-3 * np.abs(ref).max()
+
+
+@pytest.mark.parametrize("bf16", [False, True], ids=["f16", "bf16"])
+def test_mfma_pv_kat(kat, oracle, bf16):
+    """PV-MMA pattern of test_copy_srm.cu:1247-1298: p = 0.02(m+1) - 0.01(k+1) + 0.003,
+    v = 0.05(row+1) + 0.01(col+1) - 0.002, C = 0."""
+    print(f"case mfma pv bf16={bf16}", flush=True)
+    m = np.arange(32)[:, None]
+    k = np.arange(16)[None, :]
+    P = 0.02 * (m + 1) - 0.01 * (k + 1) + 0.003
+    row = np.arange(16)[:, None]
+    col = np.arange(32)[None, :]
+    V = 0.05 * (row + 1) + 0.01 * (col + 1) - 0.002
+    pv, p = _bits(P, bf16, oracle)
+    vv, v = _bits(V, bf16, oracle)
+    d = _run(kat, bf16, p, v, np.zeros((32, 32)))
+    ref = pv.astype(np.float64) @ vv.astype(np.float64)
+    assert np.abs(d - ref).max() <= 1e-2
+
+
+def test_ds_read_tr16_lane_map(kat):
+    """Within each 16-lane group G, lane i receives element (i & 3) of the four
+    16-bit words addressed by lane G + 4e + ((i % 16) >> 2), e = 0..3."""
+    print("case ds_read_b64_tr_b16 lane map", flush=True)
+    out = np.zeros((64, 4), np.int16)
+    rc = kat.kat_ds_read_tr16(out.ctypes.data_as(ctypes.POINTER(ctypes.c_int16)))
+    assert rc == 0
+    for i in range(64):
+        G = 16 * (i // 16)
+        for e in range(4):
+            j = G + 4 * e + ((i % 16) >> 2)
+            assert out[i, e] == 4 * j + (i & 3), (i, e, out[i, e])

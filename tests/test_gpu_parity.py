@@ -1,0 +1,187 @@
+"""GPU parity of the HIP forward against the CPU oracle.
+
+Every test here runs the product path (flash_attention_runtime -> _C ->
+libfa_mi355x.so C ABI -> HIP kernel) on cuda:0 and checks it against
+oracle/ (fp64 exact attention, and the emulator of the reference kernel's
+numerics for the "no worse than 2x the reference kernel's error" bar).
+
+Tolerances: O max-abs <= 1e-2, mean-abs <= 1e-3 against
+fp64 softmax(Q K^T * scale [+ causal]) V on the same quantised inputs; LSE
+abs error <= 1e-3; and O errors <= 2x the emulated reference-kernel errors
+(plus a 1e-6 floor for exact cases).
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import (CONFIGS, LSE_TOL, MAX_ABS_TOL, MEAN_ABS_TOL, case_seed, err_stats,
+                     make_config, make_qkv, to_np32)
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def _note(msg):
+    print(msg, flush=True)
+
+
+def _fwd(fa, q, k, v, causal, scale=None):
+    o, lse = fa.forward(q, k, v, causal=causal, softmax_scale=scale, return_lse=True)
+    torch.cuda.synchronize()
+    return o, lse
+
+
+def _check_against_oracle(oracle, q, k, v, o, lse, causal, scale, dtype):
+    qn, kn, vn = to_np32(q), to_np32(k), to_np32(v)
+    ref_o, ref_lse = oracle.attn_f64(qn, kn, vn, scale, causal)
+    emu_o, _ = oracle.kernel_numerics(qn, kn, vn, scale, causal,
+                                      oracle.BF16 if dtype == "bf16" else oracle.F16)
+    mx, mean = err_stats(to_np32(o), ref_o)
+    emx, emean = err_stats(emu_o, ref_o)
+    lse_err = float(np.abs(to_np32(lse).astype(np.float64) - ref_lse).max())
+    _note(f"  max_abs={mx:.3e} mean_abs={mean:.3e} (ref-kernel emu {emx:.3e}/{emean:.3e}) "
+          f"lse_err={lse_err:.3e}")
+    assert np.isfinite(to_np32(o)).all()
+    assert mx <= MAX_ABS_TOL, f"max-abs {mx}"
+    assert mean <= MEAN_ABS_TOL, f"mean-abs {mean}"
+    assert mx <= 2 * emx + 1e-6, f"max-abs {mx} > 2x reference-kernel error {emx}"
+    assert mean <= 2 * emean + 1e-6, f"mean-abs {mean} > 2x reference-kernel error {emean}"
+    assert lse_err <= LSE_TOL, f"lse {lse_err}"
+
+
+SMALL_N = [1, 2, 31, 63, 64, 65, 127, 128, 129, 200, 257, 384]
+
+
+@pytest.mark.parametrize("causal", [False, True], ids=["noncausal", "causal"])
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("N", SMALL_N)
+def test_small_shapes_vs_oracle(fa, oracle, N, D, dtype, causal):
+    _note(f"case small N={N} D={D} {dtype} causal={causal}")
+    q, k, v = make_qkv(1, 2, N, D, dtype, seed=case_seed(N * 7 + D), device="cpu")
+    scale = 1.0 / math.sqrt(D)
+    o, lse = _fwd(fa, q.to(DEV), k.to(DEV), v.to(DEV), causal)
+    _check_against_oracle(oracle, q, k, v, o, lse, causal, scale, dtype)
+
+
+def test_config_c1_full_vs_oracle(fa, oracle):
+    """C1 (the reference's CPU-runnable case) end to end, every row."""
+    q, k, v, causal, scale = make_config("C1")
+    _note("case C1 1x2x128x64 fp16")
+    o, lse = _fwd(fa, q.to(DEV), k.to(DEV), v.to(DEV), causal)
+    _check_against_oracle(oracle, q, k, v, o, lse, causal, scale, "fp16")
+
+
+def _sample_rows(N, H_total, rng, n_random=48):
+    rows = {0, 1, 2, 63, 64, 65, 127, 128, N - 1, N - 2, N // 2}
+    rows |= set(rng.integers(0, N, size=n_random).tolist())
+    rows = sorted(r for r in rows if 0 <= r < N)
+    heads = sorted({0, H_total - 1, H_total // 2})
+    sel_bh = np.array([h for h in heads for _ in rows], np.int32)
+    sel_row = np.array([r for _ in heads for r in rows], np.int32)
+    return heads, sel_bh, sel_row
+
+
+@pytest.mark.parametrize("name", ["C2", "C3", "C4", "C5", "C5r"])
+def test_config_sampled_rows_vs_oracle(fa, oracle, name):
+    """Full-size BASELINE configs: selected rows of selected heads against the
+    fp64 oracle, and the whole output against the convex-hull bound."""
+    B, H, N, D, dtype, causal, sigma, case = CONFIGS[name]
+    _note(f"case {name} {B}x{H}x{N}x{D} {dtype} causal={causal}")
+    q, k, v, causal, scale = make_config(name, device=DEV)
+    o, lse = _fwd(fa, q, k, v, causal)
+    assert torch.isfinite(o).all().item()
+    assert torch.isfinite(lse).all().item()
+
+    rng = np.random.default_rng(case)
+    heads, sel_bh, sel_row = _sample_rows(N, B * H, rng)
+    # Oracle inputs: only the selected heads (flattened b*H + h).
+    qf = q.reshape(B * H, N, D)
+    kf = k.reshape(B * H, N, D)
+    vf = v.reshape(B * H, N, D)
+    hsel = torch.tensor(heads, device=DEV)
+    qn = to_np32(qf[hsel])[None]
+    kn = to_np32(kf[hsel])[None]
+    vn = to_np32(vf[hsel])[None]
+    remap = {h: i for i, h in enumerate(heads)}
+    local_bh = np.array([remap[h] for h in sel_bh], np.int32)
+    ref_o, ref_lse = oracle.attn_rows_f64(qn, kn, vn, scale, causal, local_bh, sel_row)
+    got_o = to_np32(o.reshape(B * H, N, D)[torch.tensor(sel_bh, device=DEV).long(),
+                                           torch.tensor(sel_row, device=DEV).long()])
+    got_lse = to_np32(lse.reshape(B * H, N)[torch.tensor(sel_bh, device=DEV).long(),
+                                            torch.tensor(sel_row, device=DEV).long()])
+    mx, mean = err_stats(got_o, ref_o)
+    lse_err = float(np.abs(got_lse.astype(np.float64) - ref_lse).max())
+    _note(f"  sampled {len(sel_row)} rows: max_abs={mx:.3e} mean_abs={mean:.3e} lse={lse_err:.3e}")
+    assert mx <= MAX_ABS_TOL
+    assert mean <= MEAN_ABS_TOL
+    assert lse_err <= LSE_TOL
+
+    # Every O row is a convex combination of the visible V rows: per head dim,
+    # it lies within [min, max] of V over those rows (prefix for causal).
+    vf32 = v.float()
+    if causal:
+        vmax = torch.cummax(vf32, dim=2).values
+        vmin = torch.cummin(vf32, dim=2).values
+    else:
+        vmax = vf32.amax(dim=2, keepdim=True)
+        vmin = vf32.amin(dim=2, keepdim=True)
+    of = o.float()
+    margin = 4e-3 * torch.maximum(vmax.abs(), vmin.abs()) + 1e-3
+    assert bool((of <= vmax + margin).all().item()), "O above the convex hull of V"
+    assert bool((of >= vmin - margin).all().item()), "O below the convex hull of V"
+
+
+@pytest.mark.parametrize("name", ["C2", "C3", "C4", "C5r"])
+def test_config_zero_query_closed_form(fa, name):
+    """Q = 0 makes every visible score 0: O_i = mean of the visible V rows
+    (prefix mean when causal) and LSE_i = ln(#visible keys), at full size."""
+    B, H, N, D, dtype, causal, sigma, case = CONFIGS[name]
+    _note(f"case zero-Q {name}")
+    _, k, v, causal, scale = make_config(name, device=DEV)
+    q = torch.zeros_like(k)
+    o, lse = _fwd(fa, q, k, v, causal)
+    vd = v.double()
+    if causal:
+        cnt = torch.arange(1, N + 1, device=DEV, dtype=torch.float64)
+        ref = vd.cumsum(dim=2) / cnt[None, None, :, None]
+        ref_lse = torch.log(cnt)[None, None, :].expand(B, H, N)
+    else:
+        ref = vd.mean(dim=2, keepdim=True).expand_as(vd)
+        ref_lse = torch.full((B, H, N), math.log(N), device=DEV, dtype=torch.float64)
+    d = (o.double() - ref).abs()
+    lse_err = (lse.double() - ref_lse).abs().max().item()
+    _note(f"  max_abs={d.max().item():.3e} mean_abs={d.mean().item():.3e} lse={lse_err:.3e}")
+    assert d.max().item() <= MAX_ABS_TOL
+    assert d.mean().item() <= MEAN_ABS_TOL
+    assert lse_err <= LSE_TOL
+
+
+@pytest.mark.parametrize("name", ["C3", "C4"])
+def test_config_deterministic(fa, name):
+    """Two runs on the same inputs are bitwise identical."""
+    _note(f"case determinism {name}")
+    q, k, v, causal, scale = make_config(name, device=DEV)
+    o1, l1 = _fwd(fa, q, k, v, causal)
+    o2, l2 = _fwd(fa, q, k, v, causal)
+    assert torch.equal(o1, o2)
+    assert torch.equal(l1, l2)
+
+
+def test_key_permutation_invariance(fa):
+    """Non-causal attention is invariant under a joint permutation of the K
+    and V rows (up to fp32 summation order)."""
+    _note("case key permutation C2")
+    q, k, v, causal, scale = make_config("C2", device=DEV)
+    perm = torch.randperm(k.shape[2], generator=torch.Generator().manual_seed(7)).to(DEV)
+    o1, l1 = _fwd(fa, q, k, v, False)
+    o2, l2 = _fwd(fa, q, k[:, :, perm], v[:, :, perm], False)
+    d = (o1.float() - o2.float()).abs()
+    assert d.max().item() <= 4e-3
+    assert d.mean().item() <= 1e-4
+    assert (l1 - l2).abs().max().item() <= 1e-4
