@@ -1,0 +1,221 @@
+"""Benchmark of the MI355X FlashAttention-2 forward (BASELINE.json metric).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload C3]
+                    [--no-cpu-baseline] [--all]
+
+A step is one forward over one batch of synthetic input already resident in
+HBM: flash_attention_runtime.forward(q, k, v, o) on the headline workload C3
+(B=4, H=32, N=4096, D=128, fp16, non-causal; Q, K, V ~ N(0, 1) from seed
+1234 + 100003*2, the reference's convention in
+benchmark/python/input_data.py:11-30).  W untimed warmup steps, then K steps
+timed by two HIP events on the stream the kernel is launched on, bracketed by
+device synchronisation.  FLOPs per step = 4*B*H*N^2*D (halved for causal).
+
+Prints one JSON line with the metric, the roofline of the kernel (MFMA bound,
+against MI355X's published dense fp16/bf16 peak of 2.5 PFLOP/s) and a CPU
+baseline: the reference's CPU path (cpu_reference_attention,
+benchmark/cpp/correctness_v6.cu:23-72, restated in oracle/attn_oracle.c)
+timed on a bounded sample of rows of the same workload on the host cores.
+
+--all additionally times every BASELINE config and prints a table to stderr.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+REPO_ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(REPO_ROOT, "flash-attention_amd"))
+sys.path.insert(0, REPO_ROOT)
+
+PEAK_FP16_TFLOPS = 2500.0  # MI355X published dense fp16/bf16 MFMA peak
+PEAK_HBM_GBPS = 8000.0
+
+# id: (B, H, N, D, dtype, causal, qk_sigma, case_index)  — BASELINE.json configs
+WORKLOADS = {
+    "C2": (4, 16, 1024, 64, "fp16", False, 1.0, 1),
+    "C3": (4, 32, 4096, 128, "fp16", False, 1.0, 2),
+    "C4": (2, 32, 8192, 128, "bf16", True, 1.0, 3),
+    "C5": (1, 16, 16384, 128, "fp16", True, 3.0, 4),
+    "C5r": (1, 16, 3000, 128, "fp16", True, 3.0, 5),
+}
+TRAFFIC_FILE = os.path.join(REPO_ROOT, "profiles", "fa_fwd_C3_traffic.json")
+
+
+def flops(B, H, N, D, causal):
+    f = 4.0 * B * H * N * N * D
+    return f / 2 if causal else f
+
+
+def make_inputs(torch, name, device):
+    B, H, N, D, dtype, causal, sigma, case = WORKLOADS[name]
+    gen = torch.Generator(device=device)
+    gen.manual_seed(1234 + 100003 * case)
+    td = {"fp16": torch.float16, "bf16": torch.bfloat16}[dtype]
+    qkv = []
+    for i in range(3):
+        t = torch.randn((B, H, N, D), generator=gen, device=device, dtype=torch.float32)
+        if i < 2 and sigma != 1.0:
+            t = t * sigma
+        qkv.append(t.to(td))
+    return qkv, causal
+
+
+def time_workload(torch, fa, name, steps, warmup):
+    (q, k, v), causal = make_inputs(torch, name, "cuda")
+    o = torch.empty_like(q)
+    for _ in range(warmup):
+        fa.forward(q, k, v, o, causal=causal)
+    stream = torch.cuda.current_stream()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start.record(stream)
+    for _ in range(steps):
+        fa.forward(q, k, v, o, causal=causal)
+    stop.record(stream)
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3
+    ms = start.elapsed_time(stop) / steps
+    B, H, N, D = q.shape
+    tflops = flops(B, H, N, D, causal) / (ms * 1e-3) / 1e12
+    return ms, tflops, wall_ms
+
+
+def cpu_baseline(name, budget_s=12.0):
+    """Times the reference CPU path (oracle_ref_online_f32: fp32 online softmax
+    with expf, one query row at a time) on the first rows of the workload, on
+    all host threads OpenMP gives it; returns TFLOP/s of the same metric."""
+    import numpy as np
+    import torch
+
+    from oracle import oracle as O
+
+    B, H, N, D, dtype, causal, sigma, case = WORKLOADS[name]
+    (q, k, v), _ = make_inputs(torch, name, "cpu")
+    flat = [t.reshape(1, B * H, N, D) for t in (q, k, v)]
+    threads = O.num_threads()
+    scale = 1.0 / math.sqrt(D)
+
+    def run(rows):
+        nh = min(B * H, -(-rows // N))  # heads the rows span
+        qn, kn, vn = (t[:, :nh].float().numpy() for t in flat)
+        t0 = time.perf_counter()
+        O.ref_online_f32(qn, kn, vn, scale, causal, 0, rows)
+        return time.perf_counter() - t0, nh
+
+    # calibrate (grow the sample until it takes >= 0.3 s), then size to budget_s
+    rows = max(threads, 8)
+    while True:
+        dt, _ = run(rows)
+        if dt >= 0.3 or rows >= B * H * N:
+            break
+        rows = min(B * H * N, rows * 4)
+    rows = int(min(B * H * N, max(rows, rows * budget_s / max(dt, 1e-6))))
+    dt, nh = run(rows)
+    # FLOPs of those rows under the metric's convention (4*N*D per row,
+    # halved-on-average for causal is not applied to a row sample: use the
+    # visible key count of each row).
+    if causal:
+        keys = sum(min(N, (r % N) + 1) for r in range(rows))
+    else:
+        keys = rows * N
+    f = 4.0 * keys * D
+    return {
+        "value": f / dt / 1e12,
+        "unit": "TFLOPS",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"first {rows} query rows (the first {nh} of {B * H} heads) of {name} "
+                   f"({keys * D * 4:.3g} flop), "
+                   f"fp32 online softmax with expf as correctness_v6.cu:23-72, "
+                   f"{threads} OpenMP threads, {dt:.1f} s"),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser(description="MI355X FlashAttention-2 forward benchmark")
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="C3", choices=sorted(WORKLOADS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--all", action="store_true", help="also time every config (stderr table)")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
+              "the forward shards over (batch, head) with no communication, so N GPUs "
+              "would each run this same single-GPU benchmark on their share.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import flash_attention_runtime as fa
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+
+    name = args.workload
+    B, H, N, D, dtype, causal, sigma, case = WORKLOADS[name]
+    ms, tflops, wall_ms = time_workload(torch, fa, name, args.steps, args.warmup)
+    info = fa.device_info(0)
+
+    traffic = None
+    if os.path.exists(TRAFFIC_FILE) and name == "C3":
+        with open(TRAFFIC_FILE) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+
+    if args.all:
+        print(f"{'cfg':5s} {'ms':>9s} {'TFLOPS':>9s} {'%peak':>7s}", file=sys.stderr)
+        for wn in WORKLOADS:
+            wms, wtf, _ = time_workload(torch, fa, wn, max(10, args.steps // 2), args.warmup)
+            print(f"{wn:5s} {wms:9.4f} {wtf:9.1f} {100 * wtf / PEAK_FP16_TFLOPS:6.1f}%",
+                  file=sys.stderr, flush=True)
+
+    cpu = None if args.no_cpu_baseline else cpu_baseline(name)
+
+    line = {
+        "metric": "fwd TFLOPS + % of FP16 MFMA peak, B4 H32 N4096 D128 fp16 (1 GPU)",
+        "value": round(tflops, 2),
+        "unit": "TFLOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": dtype,
+        "data": "synthetic: Q,K,V ~ N(0,1) seeded (input_data.py random mode), resident in HBM",
+        "config": {
+            "workload": f"{name}: B={B} H={H} N={N} D={D} {dtype} "
+                        f"{'causal' if causal else 'non-causal'} FA2 forward",
+            "batch": B, "heads": H, "seq_len": N, "head_dim": D, "causal": causal,
+            "parallelism": "single GPU",
+        },
+        "pct_of_peak": round(100.0 * tflops / PEAK_FP16_TFLOPS, 2),
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(tflops, 2),
+            "peak": PEAK_FP16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(tflops / PEAK_FP16_TFLOPS, 4),
+            "traffic": traffic,
+        },
+        "cpu_baseline": cpu,
+        "device": {k: info[k] for k in ("arch", "compute_units", "clock_khz",
+                                        "fp16_dense_peak_tflops")},
+        "wall_ms_timed_region": round(wall_ms, 2),
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -51,11 +51,15 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef short i16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4_t;
 typedef __attribute__((address_space(3))) i16x8 lds_i16x8_t;
 
-constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kNumXcd = 8;  // MI355X: 8 XCDs, blocks dispatched round-robin
 
 template <bool BF16>
@@ -79,14 +83,29 @@ struct ElemOps<true> {
   }
 };
 
-// Two fp32 -> packed pair of the element type, round-to-nearest-even.
+// Two fp32 -> packed pair of the element type, round-to-nearest-even
+// (one v_cvt_pk_f16_f32 / v_cvt_pk_bf16_f32).
 template <bool BF16>
 __device__ __forceinline__ uint32_t pack2(float x, float y) {
-  using S = typename ElemOps<BF16>::scalar;
-  S a = static_cast<S>(x);
-  S b = static_cast<S>(y);
-  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, a)) |
-         (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, b)) << 16);
+  const f32x2 f = {x, y};
+  if constexpr (BF16) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2));
+  } else {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, f16x2));
+  }
+}
+
+// acc + lo(w) + hi(w) for a packed pair w of the element type, accumulated in
+// fp32 (v_dot2c_f32_f16 / v_dot2c_f32_bf16 against (1, 1)).
+template <bool BF16>
+__device__ __forceinline__ float dot2_acc(uint32_t w, float acc) {
+  if constexpr (BF16) {
+    const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w), one, acc, false);
+  } else {
+    const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w), one, acc, false);
+  }
 }
 
 // Compile-time loop: f(std::integral_constant<int, I>) for I in [B, E).
@@ -143,19 +162,19 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(const lds_void_t*)(p);
 }
 
-// One global_load_lds_dwordx4: lane i copies 16 bytes from its own `src` to
-// LDS byte address lds_base + 16*i (lds_base is wave-uniform, passed in M0).
+// One global_load_lds_dwordx4: lane i copies 16 bytes from
+// sbase + voff (voff: this lane's 32-bit byte offset) to LDS byte address
+// lds_base + 16*i (lds_base is wave-uniform, passed in M0).
 // Issued from inline asm on purpose: the compiler cannot tell which LDS
 // bytes an in-flight DMA writes, so with the builtin it would put a full
-// vmcnt(0) wait in front of every later LDS read of the *other* buffer,
-// serialising the prefetch.  The kernel instead orders the DMA explicitly:
+// vmcnt(0) wait in front of later LDS reads of the *other* buffer,
+// serialising the prefetch.  The kernel orders the DMA explicitly instead:
 // each tile ends with s_waitcnt vmcnt(0) followed by a workgroup barrier
 // before any wave reads the freshly written buffer.
-__device__ __forceinline__ void dma_16b(const void* src, const void* lds_dst_wave_base) {
-  const uint32_t base = __builtin_amdgcn_readfirstlane(lds_addr(lds_dst_wave_base));
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+__device__ __forceinline__ void dma_16b(uint32_t voff, const char* sbase, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
                :
-               : "v"(src), "s"(base)
+               : "v"(voff), "s"(sbase), "s"(lds_base)
                : "memory", "m0");
 }
 
@@ -168,6 +187,7 @@ __device__ __forceinline__ void dma_16b(const void* src, const void* lds_dst_wav
 // through the result registers so no consumer can be scheduled above it.
 template <int OFF0, int OFF1>
 __device__ __forceinline__ i16x8 ds_read_tr_pair(uint32_t addr) {
+  static_assert(OFF0 >= 0 && OFF1 < 65536, "ds offset field is 16 bits");
   i16x4 lo, hi;
   asm volatile("ds_read_b64_tr_b16 %0, %2 offset:%3\n\t"
                "ds_read_b64_tr_b16 %1, %2 offset:%4"
@@ -177,33 +197,28 @@ __device__ __forceinline__ i16x8 ds_read_tr_pair(uint32_t addr) {
   return i16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
-// Stage rows [row0, row0+64) of one head of K (or V) into an LDS tile with
-// global_load_lds_dwordx4.  Lane i of a wave instruction lands at
-// base + 16*i, so the swizzle is applied on the source side: the lane that
-// fills physical chunk pc of row r reads logical chunk pc ^ swz(r).
+// Where lane `lane` of wave `wave` lands in a K/V LDS tile for DMA
+// instruction `it`: tile row r and the logical 16-byte chunk it must fetch
+// (the XOR swizzle is applied on the source side because a DMA lane's LDS
+// destination is fixed at base + 16*lane).
 template <int D, int NW, bool IS_V>
-__device__ __forceinline__ void stage_tile(const char* __restrict__ gbase, int64_t row_stride_b,
-                                           int row0, int n_rows, char* lds_tile, int wave,
-                                           int lane) {
+__device__ __forceinline__ void dma_slot(int wave, int it, int lane, int& r, int& c) {
   using T = Tile<D>;
   constexpr int ITERS = T::BYTES / (1024 * NW);
-  static_assert(ITERS >= 1 && T::BYTES % (1024 * NW) == 0, "tile must split evenly over waves");
-#pragma unroll
-  for (int it = 0; it < ITERS; ++it) {
-    const int inst = wave * ITERS + it;
-    const int off = inst * 1024 + lane * 16;
-    const int r = off / T::ROWB;
-    const int pc = (off % T::ROWB) / 16;
-    const int c = pc ^ (IS_V ? T::swz_v(r) : T::swz_k(r));
-    int grow = row0 + r;
-    grow = grow < n_rows ? grow : n_rows - 1;
-    const char* src = gbase + grow * row_stride_b + c * 16;
-    dma_16b(src, lds_tile + inst * 1024);
-  }
+  const int off = (wave * ITERS + it) * 1024 + lane * 16;
+  r = off / T::ROWB;
+  const int pc = (off % T::ROWB) / 16;
+  c = pc ^ (IS_V ? T::swz_v(r) : T::swz_k(r));
 }
 
+// Exponent offset threshold (log2 units) for the lazy rescale: the max used
+// in p = exp2(s*c - m*c) is only raised when a row's new max exceeds it by
+// more than this, so p <= 2^8 between rescales (safe in fp16/bf16 P and in
+// the fp32 O and l accumulators) and O/l are rescaled only on such raises.
+constexpr float kRescaleThreshold = 8.0f;
+
 template <int D, bool BF16, bool CAUSAL, int NW>
-__global__ void __launch_bounds__(NW * 64)
+__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
     fa_fwd_kernel(const KernelArgs args) {
   using T = Tile<D>;
   using Ops = ElemOps<BF16>;
@@ -211,18 +226,18 @@ __global__ void __launch_bounds__(NW * 64)
   constexpr int BN = T::BN;
   constexpr int KSTEPS = D / 16;  // MFMA k-steps for S^T (k = head dim)
   constexpr int DBLK = D / 32;    // 32-wide head-dim blocks of O^T
+  constexpr int ITERS = T::BYTES / (1024 * NW);  // DMA instructions per wave per tile
+  static_assert(ITERS >= 1 && T::BYTES % (1024 * NW) == 0, "tile must split evenly over waves");
 
-  __shared__ __attribute__((aligned(1024))) char smem[4 * T::BYTES];
   // LDS ring: K buffers 0/1 then V buffers 0/1.
-  auto k_lds = [&](int i) { return smem + i * T::BYTES; };
-  auto v_lds = [&](int i) { return smem + (2 + i) * T::BYTES; };
+  __shared__ __attribute__((aligned(1024))) char smem[4 * T::BYTES];
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l32 = lane & 31;
-  const int g = lane >> 5;        // which half of the wave
-  const int lj = lane & 15;       // lane within its 16-lane group
-  const int hg = (lane >> 4) & 1; // 16-lane group within the half
+  const int g = lane >> 5;         // which half of the wave
+  const int lj = lane & 15;        // lane within its 16-lane group
+  const int hg = (lane >> 4) & 1;  // 16-lane group within the half
 
   const int N = args.seq_len;
   const int logical = xcd_remap(blockIdx.x, gridDim.x);
@@ -249,9 +264,49 @@ __global__ void __launch_bounds__(NW * 64)
   const int kv_end = CAUSAL ? min(N, q0 + BM) : N;
   const int n_tiles = (kv_end + BN - 1) / BN;
 
+  // ---- DMA plan: per-lane 32-bit source offsets within a tile ----
+  uint32_t k_src[ITERS], v_src[ITERS];
+#pragma unroll
+  for (int it = 0; it < ITERS; ++it) {
+    int r, c;
+    dma_slot<D, NW, false>(wave, it, lane, r, c);
+    k_src[it] = (uint32_t)(r * ksb + c * 16);
+    dma_slot<D, NW, true>(wave, it, lane, r, c);
+    v_src[it] = (uint32_t)(r * vsb + c * 16);
+  }
+  const uint32_t smem_base = __builtin_amdgcn_readfirstlane(lds_addr(smem));
+  const uint32_t wave_dma_base = smem_base + wave * ITERS * 1024;
+
+  // Stage K and V rows [t*BN, t*BN + BN) into LDS buffer `buf`.
+  auto issue_tile = [&](int t, int buf) {
+    const int row0 = t * BN;
+    const char* kbase = kh + row0 * ksb;
+    const char* vbase = vh + row0 * vsb;
+    const uint32_t kdst = wave_dma_base + buf * T::BYTES;
+    const uint32_t vdst = wave_dma_base + (2 + buf) * T::BYTES;
+    if (row0 + BN <= N) {
+#pragma unroll
+      for (int it = 0; it < ITERS; ++it) dma_16b(k_src[it], kbase, kdst + it * 1024);
+#pragma unroll
+      for (int it = 0; it < ITERS; ++it) dma_16b(v_src[it], vbase, vdst + it * 1024);
+    } else {
+      // ragged tail: rows past N re-read row N-1 (their scores are masked)
+      const int last = N - 1 - row0;
+#pragma unroll
+      for (int it = 0; it < ITERS; ++it) {
+        int r, c;
+        dma_slot<D, NW, false>(wave, it, lane, r, c);
+        r = r < last ? r : last;
+        dma_16b((uint32_t)(r * ksb + c * 16), kbase, kdst + it * 1024);
+        dma_slot<D, NW, true>(wave, it, lane, r, c);
+        r = r < last ? r : last;
+        dma_16b((uint32_t)(r * vsb + c * 16), vbase, vdst + it * 1024);
+      }
+    }
+  };
+
   // Start streaming tile 0 while Q is fetched into registers.
-  stage_tile<D, NW, false>(kh, ksb, 0, N, k_lds(0), wave, lane);
-  stage_tile<D, NW, true>(vh, vsb, 0, N, v_lds(0), wave, lane);
+  issue_tile(0, 0);
 
   // Q as the B operand of S^T = K Q^T: lane holds query qrow, dims
   // [16*kk + 8*g, +8) for k-step kk.
@@ -269,133 +324,145 @@ __global__ void __launch_bounds__(NW * 64)
   for (int db = 0; db < DBLK; ++db)
 #pragma unroll
     for (int i = 0; i < 16; ++i) o_acc[db][i] = 0.0f;
-  float m_run = -INFINITY;  // running max of raw scores (this query row)
-  float l_run = 0.0f;       // this lane's partial sum of p
   const float c = args.scale_log2;
+  float m_run = -INFINITY;  // max used in the exponent (<= true running max + threshold)
+  float neg_mc = 0.0f;      // -m_run * c (0 while m_run = -inf)
+  float l_run0 = 0.0f, l_run1 = 0.0f;  // this lane's partial sums of P
 
   // Per-lane LDS byte offsets inside a tile (loop invariant).
   // K: A operand of key block kb, k-step kk -> row kb*32 + l32, chunk 2kk+g.
   int k_off[KSTEPS];
-  {
-    const int key = l32;  // kb adds 32 rows = 32*ROWB bytes; swizzle uses key%16 or (key>>1)%8
 #pragma unroll
-    for (int kk = 0; kk < KSTEPS; ++kk)
-      k_off[kk] = key * T::ROWB + (((2 * kk + g) ^ T::swz_k(key)) << 4);
-  }
+  for (int kk = 0; kk < KSTEPS; ++kk)
+    k_off[kk] = l32 * T::ROWB + (((2 * kk + g) ^ T::swz_k(l32)) << 4);
   // V^T: transposed read for 16-key chunk ch, half hf, head-dim block db:
   // this lane supplies row key = 16ch + 8hf + 4g + (lj>>2) and
   // columns 32db + 16hg + 4(lj&3) .. +3.
-  int v_off[DBLK];
+  uint32_t v_addr[DBLK];
   {
     const int key = 4 * g + (lj >> 2);  // + 16ch + 8hf: multiples of 4 keep swz_v
 #pragma unroll
     for (int db = 0; db < DBLK; ++db) {
       const int col = 32 * db + 16 * hg + 4 * (lj & 3);
       const int chunk = col >> 3;
-      v_off[db] = key * T::ROWB + ((chunk ^ T::swz_v(key)) << 4) + (col & 7) * 2;
+      v_addr[db] = smem_base + key * T::ROWB + ((chunk ^ T::swz_v(key)) << 4) + (col & 7) * 2;
     }
   }
 
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
-  for (int t = 0; t < n_tiles; ++t) {
-    const int buf = t & 1;
-    if (t + 1 < n_tiles) {
-      stage_tile<D, NW, false>(kh, ksb, (t + 1) * BN, N, k_lds(buf ^ 1), wave, lane);
-      stage_tile<D, NW, true>(vh, vsb, (t + 1) * BN, N, v_lds(buf ^ 1), wave, lane);
-    }
+  auto compute_tile = [&](auto buf_c, int t) {
+    constexpr int BUF = decltype(buf_c)::value;
     const int kt0 = t * BN;
-    // Skip tiles whose every key lies after every row of this wave.
-    const bool wave_active = !CAUSAL || kt0 <= wrow0 + 31;
-    if (wave_active) {
-      const char* kt = k_lds(buf);
-      const char* vt = v_lds(buf);
+    const char* kt = smem + BUF * T::BYTES;
 
-      // ---- S^T = K Q^T : two 32-key blocks ----
-      f32x16 s[2];
+    // ---- S^T = K Q^T : two 32-key blocks ----
+    f32x16 s[2];
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
+    for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) s[kb][i] = 0.0f;
+      for (int i = 0; i < 16; ++i) s[kb][i] = 0.0f;
 #pragma unroll
-        for (int kk = 0; kk < KSTEPS; ++kk) {
-          const i16x8 a = *reinterpret_cast<const i16x8*>(kt + kb * 32 * T::ROWB + k_off[kk]);
-          s[kb] = Ops::mfma(a, qf[kk], s[kb]);
-        }
-      }
+    for (int kk = 0; kk < KSTEPS; ++kk) {
+      const i16x8 a0 = *reinterpret_cast<const i16x8*>(kt + k_off[kk]);
+      const i16x8 a1 = *reinterpret_cast<const i16x8*>(kt + 32 * T::ROWB + k_off[kk]);
+      s[0] = Ops::mfma(a0, qf[kk], s[0]);
+      s[1] = Ops::mfma(a1, qf[kk], s[1]);
+    }
 
-      // ---- masking (ragged tail / causal diagonal) ----
-      const bool need_mask = (kt0 + BN > N) || (CAUSAL && kt0 + BN - 1 > wrow0);
-      if (need_mask) {
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const int key = kt0 + kb * 32 + 8 * (i >> 2) + 4 * g + (i & 3);
-            const bool masked = key >= N || (CAUSAL && key > qrow);
-            if (masked) s[kb][i] = -INFINITY;
-          }
-      }
-
-      // ---- online softmax (reference online_softmax.cuh:89-152) ----
-      float mx = s[0][0];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[kb][i]);
-      mx = fmaxf(mx, swap_halves(mx));
-      const float m_new = fmaxf(m_run, mx);
-      const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-      const float alpha = fast_exp2((m_run - m_use) * c);
-      const float mc = m_use * c;
-      float rs = 0.0f;
+    // ---- masking (ragged tail / causal diagonal) ----
+    const bool need_mask = (kt0 + BN > N) || (CAUSAL && kt0 + BN - 1 > wrow0);
+    if (need_mask) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          const float p = fast_exp2(fmaf(s[kb][i], c, -mc));
-          s[kb][i] = p;
-          rs += p;
+          const int key = kt0 + kb * 32 + 8 * (i >> 2) + 4 * g + (i & 3);
+          const bool masked = key >= N || (CAUSAL && key > qrow);
+          if (masked) s[kb][i] = -INFINITY;
         }
-      l_run = fmaf(l_run, alpha, rs);
+    }
+
+    // ---- online softmax with lazy rescale (reference online_softmax.cuh:89-152) ----
+    float mx = fmaxf(s[0][0], s[1][0]);
+#pragma unroll
+    for (int i = 1; i < 16; ++i) mx = fmaxf(mx, fmaxf(s[0][i], s[1][i]));
+    mx = fmaxf(mx, swap_halves(mx));
+    const bool grow = (mx - m_run) * c > kRescaleThreshold;  // false for NaN (-inf - -inf)
+    if (__any(grow)) {
+      const float m_new = grow ? mx : m_run;
+      const float alpha = grow ? fast_exp2((m_run - m_new) * c) : 1.0f;
       m_run = m_new;
+      neg_mc = -(m_run == -INFINITY ? 0.0f : m_run) * c;
+      l_run0 *= alpha;
+      l_run1 *= alpha;
 #pragma unroll
       for (int db = 0; db < DBLK; ++db)
 #pragma unroll
         for (int i = 0; i < 16; ++i) o_acc[db][i] *= alpha;
+    }
 
-      // ---- P^T as B operand: chunk ch = 2kb + hh uses S regs 8hh..8hh+7 ----
-      i16x8 pf[4];
+    // ---- P = exp2(s*c - m*c), packed as the P^T B operand ----
+    // chunk ch = 2kb + hh uses S registers 8hh..8hh+7 of block kb.
+    i16x8 pf[4];
 #pragma unroll
-      for (int ch = 0; ch < 4; ++ch) {
-        const int kb = ch >> 1, base = (ch & 1) * 8;
-        uint32_t w0 = pack2<BF16>(s[kb][base + 0], s[kb][base + 1]);
-        uint32_t w1 = pack2<BF16>(s[kb][base + 2], s[kb][base + 3]);
-        uint32_t w2 = pack2<BF16>(s[kb][base + 4], s[kb][base + 5]);
-        uint32_t w3 = pack2<BF16>(s[kb][base + 6], s[kb][base + 7]);
-        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-        u32x4 w = {w0, w1, w2, w3};
-        pf[ch] = __builtin_bit_cast(i16x8, w);
+    for (int ch = 0; ch < 4; ++ch) {
+      const int kb = ch >> 1, base = (ch & 1) * 8;
+      u32x4 w;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float p0 = fast_exp2(fmaf(s[kb][base + 2 * j], c, neg_mc));
+        const float p1 = fast_exp2(fmaf(s[kb][base + 2 * j + 1], c, neg_mc));
+        w[j] = pack2<BF16>(p0, p1);
+        if constexpr (BF16) {
+          // bf16 keeps 8 significant bits: sum the unrounded fp32 p (as the
+          // reference does, online_softmax.cuh:135-152) so the LSE stays
+          // accurate to ~1e-6 instead of ~2^-8.
+          l_run0 += p0;
+          l_run1 += p1;
+        }
       }
-
-      // ---- O^T += V^T P^T ----
-#pragma unroll
-      for (int db = 0; db < DBLK; ++db) {
-        const uint32_t addr = lds_addr(vt + v_off[db]);
-        static_for<0, 4>([&](auto ch_c) {
-          constexpr int ch = decltype(ch_c)::value;
-          const i16x8 a = ds_read_tr_pair<ch * 16 * T::ROWB, ch * 16 * T::ROWB + 8 * T::ROWB>(addr);
-          o_acc[db] = Ops::mfma(a, pf[ch], o_acc[db]);
-        });
+      pf[ch] = __builtin_bit_cast(i16x8, w);
+      if constexpr (!BF16) {
+        // fp16: sum the rounded P (the values that enter P V; relative
+        // error <= 2^-11 per term) with v_dot2c_f32_f16, 2 terms per op.
+        l_run0 = dot2_acc<BF16>(w[0], l_run0);
+        l_run1 = dot2_acc<BF16>(w[1], l_run1);
+        l_run0 = dot2_acc<BF16>(w[2], l_run0);
+        l_run1 = dot2_acc<BF16>(w[3], l_run1);
       }
     }
+
+    // ---- O^T += V^T P^T ----
+#pragma unroll
+    for (int db = 0; db < DBLK; ++db) {
+      static_for<0, 4>([&](auto ch_c) {
+        constexpr int ch = decltype(ch_c)::value;
+        constexpr int off = (2 + BUF) * T::BYTES + ch * 16 * T::ROWB;
+        const i16x8 a = ds_read_tr_pair<off, off + 8 * T::ROWB>(v_addr[db]);
+        o_acc[db] = Ops::mfma(a, pf[ch], o_acc[db]);
+      });
+    }
+  };
+
+  auto tile_step = [&](auto buf_c, int t) {
+    constexpr int BUF = decltype(buf_c)::value;
+    if (t + 1 < n_tiles) issue_tile(t + 1, BUF ^ 1);
+    // Skip tiles whose every key lies after every row of this wave.
+    if (!CAUSAL || t * BN <= wrow0 + 31) compute_tile(buf_c, t);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
+  };
+
+  for (int t = 0; t < n_tiles; t += 2) {
+    tile_step(std::integral_constant<int, 0>{}, t);
+    if (t + 1 < n_tiles) tile_step(std::integral_constant<int, 1>{}, t + 1);
   }
 
   // ---- epilogue: combine the two half-row partial sums, normalise, store ----
-  const float l_tot = l_run + swap_halves(l_run);
+  const float l_lane = l_run0 + l_run1;
+  const float l_tot = l_lane + swap_halves(l_lane);
   const bool row_ok = qrow < N;
   const float inv_l = (row_ok && l_tot > 0.0f) ? 1.0f / l_tot : 0.0f;
   if (row_ok) {
@@ -405,10 +472,8 @@ __global__ void __launch_bounds__(NW * 64)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int col = 32 * db + 8 * r + 4 * g;
-        uint32_t w0 = pack2<BF16>(o_acc[db][4 * r + 0] * inv_l, o_acc[db][4 * r + 1] * inv_l);
-        uint32_t w1 = pack2<BF16>(o_acc[db][4 * r + 2] * inv_l, o_acc[db][4 * r + 3] * inv_l);
-        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-        u32x2 w = {w0, w1};
+        u32x2 w = {pack2<BF16>(o_acc[db][4 * r + 0] * inv_l, o_acc[db][4 * r + 1] * inv_l),
+                   pack2<BF16>(o_acc[db][4 * r + 2] * inv_l, o_acc[db][4 * r + 3] * inv_l)};
         *reinterpret_cast<u32x2*>(op + col * 2) = w;
       }
     if (args.lse != nullptr && g == 0) {
