@@ -41,102 +41,14 @@
 
 #include <type_traits>
 
+#include "fa_device_ops.h"
 #include "fa_fwd_kernel.h"
 
 namespace fa {
 namespace {
 
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef short i16x4 __attribute__((ext_vector_type(4)));
-typedef short i16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) void lds_void_t;
-typedef __attribute__((address_space(3))) i16x4 lds_i16x4_t;
-typedef __attribute__((address_space(3))) i16x8 lds_i16x8_t;
+using namespace dev;
 
-constexpr int kNumXcd = 8;  // MI355X: 8 XCDs, blocks dispatched round-robin
-
-template <bool BF16>
-struct ElemOps;
-
-template <>
-struct ElemOps<false> {
-  using scalar = _Float16;
-  static __device__ __forceinline__ f32x16 mfma(i16x8 a, i16x8 b, f32x16 c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
-                                                 __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
-  }
-};
-
-template <>
-struct ElemOps<true> {
-  using scalar = __bf16;
-  static __device__ __forceinline__ f32x16 mfma(i16x8 a, i16x8 b, f32x16 c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
-                                                  __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-  }
-};
-
-// Two fp32 -> packed pair of the element type, round-to-nearest-even
-// (one v_cvt_pk_f16_f32 / v_cvt_pk_bf16_f32).
-template <bool BF16>
-__device__ __forceinline__ uint32_t pack2(float x, float y) {
-  const f32x2 f = {x, y};
-  if constexpr (BF16) {
-    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2));
-  } else {
-    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, f16x2));
-  }
-}
-
-// acc + lo(w) + hi(w) for a packed pair w of the element type, accumulated in
-// fp32 (v_dot2c_f32_f16 / v_dot2c_f32_bf16 against (1, 1)).
-template <bool BF16>
-__device__ __forceinline__ float dot2_acc(uint32_t w, float acc) {
-  if constexpr (BF16) {
-    const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
-    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w), one, acc, false);
-  } else {
-    const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
-    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w), one, acc, false);
-  }
-}
-
-// Compile-time loop: f(std::integral_constant<int, I>) for I in [B, E).
-template <int B, int E, class F>
-__device__ __forceinline__ void static_for(F&& f) {
-  if constexpr (B < E) {
-    f(std::integral_constant<int, B>{});
-    static_for<B + 1, E>(f);
-  }
-}
-
-__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
-
-// Value of lane (l ^ 32) for every lane l.
-__device__ __forceinline__ float swap_halves(float x) {
-  return __shfl_xor(x, 32, 64);
-}
-
-// Hardware dispatches workgroup b to XCD b % 8.  Map the dispatch order to a
-// logical order in which XCD x owns the contiguous logical range
-// [start_x, start_x + count_x), so the blocks that share a head's K/V run on
-// the same L2.  Bijective for any total.
-__device__ __forceinline__ int xcd_remap(int b, int total) {
-  const int per = (total + kNumXcd - 1) / kNumXcd;
-  int tall = total % kNumXcd;
-  if (tall == 0) tall = kNumXcd;
-  const int xcd = b % kNumXcd;
-  const int local = b / kNumXcd;
-  if (xcd < tall) return xcd * per + local;
-  return tall * per + (xcd - tall) * (per - 1) + local;
-}
 
 template <int D>
 struct Tile {
@@ -156,46 +68,6 @@ struct Tile {
     return D == 128 ? ((key & 3) << 2) : (((key >> 1) & 1) << 2);
   }
 };
-
-// 32-bit LDS address of a pointer into __shared__ memory.
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return (uint32_t)(uintptr_t)(const lds_void_t*)(p);
-}
-
-// One global_load_lds_dwordx4: lane i copies 16 bytes from
-// sbase + voff (voff: this lane's 32-bit byte offset) to LDS byte address
-// lds_base + 16*i (lds_base is wave-uniform, passed in M0).
-// Issued from inline asm on purpose: the compiler cannot tell which LDS
-// bytes an in-flight DMA writes, so with the builtin it would put a full
-// vmcnt(0) wait in front of later LDS reads of the *other* buffer,
-// serialising the prefetch.  The kernel orders the DMA explicitly instead:
-// each tile ends with s_waitcnt vmcnt(0) followed by a workgroup barrier
-// before any wave reads the freshly written buffer.
-__device__ __forceinline__ void dma_16b(uint32_t voff, const char* sbase, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
-               :
-               : "v"(voff), "s"(sbase), "s"(lds_base)
-               : "memory", "m0");
-}
-
-// Two ds_read_b64_tr_b16 (the gfx950 transposing LDS read) at byte
-// addresses addr+OFF0 and addr+OFF1, concatenated into one 8 x 16-bit MFMA
-// operand.  Within each 16-lane group, lane i receives element (i & 3) of
-// the 4 x 16-bit words addressed by lanes 4e + (i >> 2), e = 0..3.
-// Issued from inline asm so the compiler does not put a vmcnt(0) wait for the
-// in-flight K/V prefetch DMA in front of it; the lgkmcnt wait is chained
-// through the result registers so no consumer can be scheduled above it.
-template <int OFF0, int OFF1>
-__device__ __forceinline__ i16x8 ds_read_tr_pair(uint32_t addr) {
-  static_assert(OFF0 >= 0 && OFF1 < 65536, "ds offset field is 16 bits");
-  i16x4 lo, hi;
-  asm volatile("ds_read_b64_tr_b16 %0, %2 offset:%3\n\t"
-               "ds_read_b64_tr_b16 %1, %2 offset:%4"
-               : "=v"(lo), "=v"(hi)
-               : "v"(addr), "i"(OFF0), "i"(OFF1));
-  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(lo), "+v"(hi));
-  return i16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-}
 
 // Where lane `lane` of wave `wave` lands in a K/V LDS tile for DMA
 // instruction `it`: tile row r and the logical 16-byte chunk it must fetch
@@ -388,7 +260,7 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
     float mx = fmaxf(s[0][0], s[1][0]);
 #pragma unroll
     for (int i = 1; i < 16; ++i) mx = fmaxf(mx, fmaxf(s[0][i], s[1][i]));
-    mx = fmaxf(mx, swap_halves(mx));
+    mx = pair_max(mx);
     const bool grow = (mx - m_run) * c > kRescaleThreshold;  // false for NaN (-inf - -inf)
     if (__any(grow)) {
       const float m_new = grow ? mx : m_run;
@@ -462,7 +334,7 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
 
   // ---- epilogue: combine the two half-row partial sums, normalise, store ----
   const float l_lane = l_run0 + l_run1;
-  const float l_tot = l_lane + swap_halves(l_lane);
+  const float l_tot = pair_sum(l_lane);
   const bool row_ok = qrow < N;
   const float inv_l = (row_ok && l_tot > 0.0f) ? 1.0f / l_tot : 0.0f;
   if (row_ok) {

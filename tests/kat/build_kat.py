@@ -6,6 +6,7 @@ import os
 import subprocess
 
 HERE = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(os.path.dirname(os.path.dirname(HERE)), "flash-attention_amd", "csrc")
 SRC = os.path.join(HERE, "fa_kat.hip")
 LIB = os.path.join(HERE, "libfa_kat.so")
 
@@ -15,7 +16,7 @@ def build() -> str:
     tmp = LIB + ".tmp"
     cmd = [hipcc, "--offload-arch=gfx950", "-O2", "-std=c++17", "-fPIC", "-shared",
            "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-           "-x", "hip", SRC, "-o", tmp]
+           "-I", CSRC, "-x", "hip", SRC, "-o", tmp]
     proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
     if proc.returncode != 0:
         raise RuntimeError(proc.stdout)

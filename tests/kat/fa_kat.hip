@@ -12,33 +12,54 @@
 #include <stdint.h>
 #include <string.h>
 
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef short i16x4 __attribute__((ext_vector_type(4)));
-typedef short i16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef __attribute__((address_space(3))) i16x4 lds_i16x4_t;
+#include "fa_device_ops.h"
+
+using namespace fa::dev;
 
 __global__ void kat_mfma_kernel(const i16x8* a, const i16x8* b, const float* c, float* d, int bf16) {
   const int l = threadIdx.x;
   f32x16 acc;
   for (int i = 0; i < 16; ++i) acc[i] = c[l * 16 + i];
-  if (bf16)
-    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a[l]),
-                                                 __builtin_bit_cast(bf16x8, b[l]), acc, 0, 0, 0);
-  else
-    acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a[l]),
-                                                __builtin_bit_cast(f16x8, b[l]), acc, 0, 0, 0);
+  acc = bf16 ? ElemOps<true>::mfma(a[l], b[l], acc) : ElemOps<false>::mfma(a[l], b[l], acc);
   for (int i = 0; i < 16; ++i) d[l * 16 + i] = acc[i];
 }
 
+// ds_read_tr_pair<0, 512>: lane j addresses words 4j..4j+3 (first read) and
+// 256+4j..256+4j+3 (second read) of an LDS array holding 0..1023.
 __global__ void kat_tr_kernel(short* out) {
   __shared__ short lds[1024];
   const int l = threadIdx.x;
   for (int i = l; i < 1024; i += 64) lds[i] = (short)i;
   __syncthreads();
-  const i16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(lds + 4 * l));
-  for (int e = 0; e < 4; ++e) out[l * 4 + e] = r[e];
+  const i16x8 r = ds_read_tr_pair<0, 512>(lds_addr(lds + 4 * l));
+  for (int e = 0; e < 8; ++e) out[l * 8 + e] = r[e];
+}
+
+__global__ void kat_pack_kernel(const float* in, uint32_t* out, float* dot, int bf16) {
+  const int l = threadIdx.x;
+  const uint32_t w = bf16 ? pack2<true>(in[2 * l], in[2 * l + 1]) : pack2<false>(in[2 * l], in[2 * l + 1]);
+  out[l] = w;
+  dot[l] = bf16 ? dot2_acc<true>(w, 0.25f) : dot2_acc<false>(w, 0.25f);
+}
+
+__global__ void kat_pair_kernel(const float* in, float* mx, float* sm) {
+  const int l = threadIdx.x;
+  mx[l] = pair_max(in[l]);
+  sm[l] = pair_sum(in[l]);
+}
+
+// dma_16b: lane i fetches 16 bytes from src + 16*((i * 7) % 64) into LDS
+// bytes [16*i, 16*i + 16) of the second 1 KiB of a 2 KiB buffer.
+__global__ void kat_dma_kernel(const char* src, int* out) {
+  __shared__ __attribute__((aligned(1024))) int buf[512];
+  const int l = threadIdx.x;
+  for (int i = l; i < 512; i += 64) buf[i] = -1;
+  __syncthreads();
+  const uint32_t base = __builtin_amdgcn_readfirstlane(lds_addr(buf)) + 1024;
+  dma_16b((uint32_t)(16 * ((l * 7) % 64)), src, base);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  for (int i = l; i < 512; i += 64) out[i] = buf[i];
 }
 
 static int check(hipError_t e) { return e == hipSuccess ? 0 : (int)e; }
@@ -89,17 +110,78 @@ extern "C" int kat_mfma_32x32x16(int bf16, const uint16_t* a_bits, const uint16_
   return rc;
 }
 
-// out[64*4]: what each lane receives from ds_read_b64_tr_b16 when lane j
-// addresses the four 16-bit words 4j..4j+3 of an LDS array holding 0..1023.
+// out[64*8]: the two transposed reads of ds_read_tr_pair<0, 512> per lane.
 extern "C" int kat_ds_read_tr16(int16_t* out) {
   void* d = 0;
-  int rc = check(hipMalloc(&d, 64 * 4 * 2));
+  int rc = check(hipMalloc(&d, 64 * 8 * 2));
   if (!rc) {
     hipLaunchKernelGGL(kat_tr_kernel, dim3(1), dim3(64), 0, 0, (short*)d);
     rc = check(hipGetLastError());
   }
   if (!rc) rc = check(hipDeviceSynchronize());
-  if (!rc) rc = check(hipMemcpy(out, d, 64 * 4 * 2, hipMemcpyDeviceToHost));
+  if (!rc) rc = check(hipMemcpy(out, d, 64 * 8 * 2, hipMemcpyDeviceToHost));
   if (d) (void)hipFree(d);
+  return rc;
+}
+
+// in[128] floats -> out[64] packed pairs (pack2) and dot[64] = 0.25 + sum of
+// the pair (dot2_acc).
+extern "C" int kat_pack2(int bf16, const float* in, uint32_t* out, float* dot) {
+  void *di = 0, *dout = 0, *ddot = 0;
+  int rc = check(hipMalloc(&di, 128 * 4));
+  if (!rc) rc = check(hipMalloc(&dout, 64 * 4));
+  if (!rc) rc = check(hipMalloc(&ddot, 64 * 4));
+  if (!rc) rc = check(hipMemcpy(di, in, 128 * 4, hipMemcpyHostToDevice));
+  if (!rc) {
+    hipLaunchKernelGGL(kat_pack_kernel, dim3(1), dim3(64), 0, 0, (const float*)di,
+                       (uint32_t*)dout, (float*)ddot, bf16);
+    rc = check(hipGetLastError());
+  }
+  if (!rc) rc = check(hipDeviceSynchronize());
+  if (!rc) rc = check(hipMemcpy(out, dout, 64 * 4, hipMemcpyDeviceToHost));
+  if (!rc) rc = check(hipMemcpy(dot, ddot, 64 * 4, hipMemcpyDeviceToHost));
+  if (di) (void)hipFree(di);
+  if (dout) (void)hipFree(dout);
+  if (ddot) (void)hipFree(ddot);
+  return rc;
+}
+
+// in[64] -> pair_max / pair_sum of lanes l and l^32.
+extern "C" int kat_pair(const float* in, float* mx, float* sm) {
+  void *di = 0, *dm = 0, *ds = 0;
+  int rc = check(hipMalloc(&di, 64 * 4));
+  if (!rc) rc = check(hipMalloc(&dm, 64 * 4));
+  if (!rc) rc = check(hipMalloc(&ds, 64 * 4));
+  if (!rc) rc = check(hipMemcpy(di, in, 64 * 4, hipMemcpyHostToDevice));
+  if (!rc) {
+    hipLaunchKernelGGL(kat_pair_kernel, dim3(1), dim3(64), 0, 0, (const float*)di, (float*)dm,
+                       (float*)ds);
+    rc = check(hipGetLastError());
+  }
+  if (!rc) rc = check(hipDeviceSynchronize());
+  if (!rc) rc = check(hipMemcpy(mx, dm, 64 * 4, hipMemcpyDeviceToHost));
+  if (!rc) rc = check(hipMemcpy(sm, ds, 64 * 4, hipMemcpyDeviceToHost));
+  if (di) (void)hipFree(di);
+  if (dm) (void)hipFree(dm);
+  if (ds) (void)hipFree(ds);
+  return rc;
+}
+
+// src: 1 KiB of int32 0..255 -> out[512]: the 2 KiB LDS buffer after one DMA.
+extern "C" int kat_dma(int* out) {
+  int host[256];
+  for (int i = 0; i < 256; ++i) host[i] = i;
+  void *dsrc = 0, *dout = 0;
+  int rc = check(hipMalloc(&dsrc, 1024));
+  if (!rc) rc = check(hipMalloc(&dout, 2048));
+  if (!rc) rc = check(hipMemcpy(dsrc, host, 1024, hipMemcpyHostToDevice));
+  if (!rc) {
+    hipLaunchKernelGGL(kat_dma_kernel, dim3(1), dim3(64), 0, 0, (const char*)dsrc, (int*)dout);
+    rc = check(hipGetLastError());
+  }
+  if (!rc) rc = check(hipDeviceSynchronize());
+  if (!rc) rc = check(hipMemcpy(out, dout, 2048, hipMemcpyDeviceToHost));
+  if (dsrc) (void)hipFree(dsrc);
+  if (dout) (void)hipFree(dout);
   return rc;
 }

@@ -23,6 +23,9 @@ def kat():
     fp = ctypes.POINTER(ctypes.c_float)
     L.kat_mfma_32x32x16.argtypes = [ctypes.c_int, u16p, u16p, fp, fp]
     L.kat_ds_read_tr16.argtypes = [ctypes.POINTER(ctypes.c_int16)]
+    L.kat_pack2.argtypes = [ctypes.c_int, fp, ctypes.POINTER(ctypes.c_uint32), fp]
+    L.kat_pair.argtypes = [fp, fp, fp]
+    L.kat_dma.argtypes = [ctypes.POINTER(ctypes.c_int32)]
     return L
 
 
@@ -95,14 +98,70 @@ def test_mfma_pv_kat(kat, oracle, bf16):
 
 
 def test_ds_read_tr16_lane_map(kat):
-    """Within each 16-lane group G, lane i receives element (i & 3) of the four
-    16-bit words addressed by lane G + 4e + ((i % 16) >> 2), e = 0..3."""
+    """ds_read_tr_pair: within each 16-lane group G, lane i receives element
+    (i & 3) of the four 16-bit words addressed by lane G + 4e + ((i % 16) >> 2),
+    e = 0..3, for each of the two reads (the second at +512 bytes)."""
     print("case ds_read_b64_tr_b16 lane map", flush=True)
-    out = np.zeros((64, 4), np.int16)
+    out = np.zeros((64, 8), np.int16)
     rc = kat.kat_ds_read_tr16(out.ctypes.data_as(ctypes.POINTER(ctypes.c_int16)))
     assert rc == 0
     for i in range(64):
         G = 16 * (i // 16)
-        for e in range(4):
-            j = G + 4 * e + ((i % 16) >> 2)
-            assert out[i, e] == 4 * j + (i & 3), (i, e, out[i, e])
+        for half in range(2):
+            for e in range(4):
+                j = G + 4 * e + ((i % 16) >> 2)
+                assert out[i, 4 * half + e] == 256 * half + 4 * j + (i & 3), (i, half, e)
+
+
+@pytest.mark.parametrize("bf16", [False, True], ids=["f16", "bf16"])
+def test_pack2_rne_and_dot2(kat, oracle, bf16):
+    """pack2 rounds to nearest even exactly like the oracle's RNE conversion
+    (ties, subnormals, overflow); dot2_acc adds both halves to an fp32
+    accumulator."""
+    print(f"case pack2/dot2 bf16={bf16}", flush=True)
+    rng = np.random.default_rng(3)
+    vals = rng.standard_normal(128).astype(np.float32)
+    special = np.array([0.5 + 2 ** -12, 1 + 2 ** -11, 1 + 3 * 2 ** -11, 1 + 2 ** -8, 1 + 3 * 2 ** -8,
+                        65504.0, 65520.0, 1e-6, -2 ** -25, 3.0e-5, 1 + 2 ** -9, -1 - 3 * 2 ** -9],
+                       np.float32)
+    vals[:special.size] = special
+    out = np.zeros(64, np.uint32)
+    dot = np.zeros(64, np.float32)
+    fp = ctypes.POINTER(ctypes.c_float)
+    rc = kat.kat_pack2(int(bf16), vals.ctypes.data_as(fp),
+                       out.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)), dot.ctypes.data_as(fp))
+    assert rc == 0
+    ref_vals, ref_bits = (oracle.round_bf16 if bf16 else oracle.round_f16)(vals)
+    got_bits = np.stack([out & 0xFFFF, out >> 16], axis=1).reshape(-1).astype(np.uint16)
+    assert np.array_equal(got_bits, ref_bits)
+    pairs = ref_vals.reshape(64, 2).astype(np.float64)
+    finite = np.isfinite(pairs).all(axis=1)
+    assert np.allclose(dot[finite], 0.25 + pairs[finite].sum(axis=1), rtol=1e-6, atol=1e-6)
+
+
+def test_pair_reductions(kat):
+    """pair_max / pair_sum combine lanes l and l^32 (the two halves of one
+    query row in the 32x32 accumulator layout)."""
+    print("case pair reductions", flush=True)
+    x = np.random.default_rng(4).standard_normal(64).astype(np.float32)
+    x[5] = -np.inf
+    mx = np.zeros(64, np.float32)
+    sm = np.zeros(64, np.float32)
+    fp = ctypes.POINTER(ctypes.c_float)
+    assert kat.kat_pair(x.ctypes.data_as(fp), mx.ctypes.data_as(fp), sm.ctypes.data_as(fp)) == 0
+    partner = x[np.arange(64) ^ 32]
+    assert np.array_equal(mx, np.maximum(x, partner))
+    assert np.array_equal(sm, (x + partner).astype(np.float32))
+
+
+def test_dma_lane_placement(kat):
+    """dma_16b: lane i's 16 bytes from its own source offset land at LDS
+    base + 16*i; nothing outside the 1 KiB window is touched."""
+    print("case global_load_lds_dwordx4 placement", flush=True)
+    out = np.zeros(512, np.int32)
+    assert kat.kat_dma(out.ctypes.data_as(ctypes.POINTER(ctypes.c_int32))) == 0
+    assert np.all(out[:256] == -1)
+    lanes = np.arange(64)
+    src_chunk = (lanes * 7) % 64
+    expect = (src_chunk[:, None] * 4 + np.arange(4)[None, :]).reshape(-1)
+    assert np.array_equal(out[256:], expect)
