@@ -15,6 +15,10 @@
 
 #include <type_traits>
 
+// Kernel-local lambdas carry this so they are always inlined: an outlined
+// lambda receives its by-reference captures through scratch memory.
+#define FA_INLINE __attribute__((always_inline))
+
 namespace fa {
 namespace dev {
 
@@ -109,6 +113,31 @@ __device__ __forceinline__ float pair_max(float x) {
   pair_values(x, lo, hi);
   return fmaxf(lo, hi);
 }
+// max(a, b, c) in one v_max3_f32.  Issued from inline asm because fmaxf
+// makes the compiler quiet possible signalling NaNs with an extra v_max of
+// each MFMA result first; the scores here are never NaN.
+__device__ __forceinline__ float max3(float a, float b, float c) {
+  float d;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
+  return d;
+}
+
+// Max of the 32 values of two MFMA accumulators: a v_max3 tree of depth 4
+// (16 instructions).
+__device__ __forceinline__ float max32(const f32x16& x, const f32x16& y) {
+  float m[11];
+#pragma unroll
+  for (int i = 0; i < 5; ++i) {
+    m[i] = max3(x[3 * i], x[3 * i + 1], x[3 * i + 2]);
+    m[5 + i] = max3(y[3 * i], y[3 * i + 1], y[3 * i + 2]);
+  }
+  m[10] = max3(x[15], y[15], m[9]);
+  const float a = max3(m[0], m[1], m[2]);
+  const float b = max3(m[3], m[4], m[5]);
+  const float c = max3(m[6], m[7], m[8]);
+  return max3(a, b, max3(c, m[10], m[10]));
+}
+
 __device__ __forceinline__ float pair_sum(float x) {
   float lo, hi;
   pair_values(x, lo, hi);

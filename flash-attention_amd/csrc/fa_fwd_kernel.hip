@@ -22,6 +22,11 @@
 //    LDS ring; the loads of tile t+1 fly while tile t is computed.  Each tile
 //    carries an XOR swizzle on its 16-byte chunks chosen so the K reads
 //    (ds_read_b128) and the V transposed reads hit distinct banks.
+//  * LDS operands are read a few MFMAs ahead of use (K: 3 k-steps, V: 4
+//    MFMAs, the first V reads overlapping the softmax) so each MFMA finds its
+//    operand ready; two workgroups share a CU (2 waves per SIMD), and the
+//    wave issuing PV MFMAs runs at raised priority so the other wave's
+//    softmax fills the VALU in the meantime.
 //  * Causal: fully-masked K tiles are never loaded or computed; q-tiles are
 //    dispatched longest-first.  Ragged N: loads clamp to the last row and the
 //    scores of keys >= N are -inf; rows >= N are never stored.
@@ -89,6 +94,11 @@ __device__ __forceinline__ void dma_slot(int wave, int it, int lane, int& r, int
 // the fp32 O and l accumulators) and O/l are rescaled only on such raises.
 constexpr float kRescaleThreshold = 8.0f;
 
+// Operand prefetch depths (measured best on MI355X): K operands for S^T are
+// read 3 k-steps ahead, V^T operands 4 MFMAs ahead.
+constexpr int kKWindow = 3;
+constexpr int kVWindow = 4;
+
 template <int D, bool BF16, bool CAUSAL, int NW>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
     fa_fwd_kernel(const KernelArgs args) {
@@ -150,7 +160,7 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
   const uint32_t wave_dma_base = smem_base + wave * ITERS * 1024;
 
   // Stage K and V rows [t*BN, t*BN + BN) into LDS buffer `buf`.
-  auto issue_tile = [&](int t, int buf) {
+  auto issue_tile = [&](int t, int buf) FA_INLINE {
     const int row0 = t * BN;
     const char* kbase = kh + row0 * ksb;
     const char* vbase = vh + row0 * vsb;
@@ -162,17 +172,16 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
 #pragma unroll
       for (int it = 0; it < ITERS; ++it) dma_16b(v_src[it], vbase, vdst + it * 1024);
     } else {
-      // ragged tail: rows past N re-read row N-1 (their scores are masked)
+      // ragged tail: rows past N re-read row N-1 (their scores are masked).
+      // This lane's tile row for instruction it is it*RPI + r_lane.
+      constexpr int RPI = 1024 / T::ROWB;  // rows per DMA instruction
+      const int r_lane = (wave * ITERS) * RPI + lane / (T::ROWB / 16);
       const int last = N - 1 - row0;
 #pragma unroll
       for (int it = 0; it < ITERS; ++it) {
-        int r, c;
-        dma_slot<D, NW, false>(wave, it, lane, r, c);
-        r = r < last ? r : last;
-        dma_16b((uint32_t)(r * ksb + c * 16), kbase, kdst + it * 1024);
-        dma_slot<D, NW, true>(wave, it, lane, r, c);
-        r = r < last ? r : last;
-        dma_16b((uint32_t)(r * vsb + c * 16), vbase, vdst + it * 1024);
+        const int over = max(it * RPI + r_lane - last, 0);
+        dma_16b(k_src[it] - (uint32_t)(over * ksb), kbase, kdst + it * 1024);
+        dma_16b(v_src[it] - (uint32_t)(over * vsb), vbase, vdst + it * 1024);
       }
     }
   };
@@ -224,24 +233,54 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
-  auto compute_tile = [&](auto buf_c, int t) {
+  auto compute_tile = [&](auto buf_c, int t) FA_INLINE {
     constexpr int BUF = decltype(buf_c)::value;
     const int kt0 = t * BN;
     const char* kt = smem + BUF * T::BYTES;
 
     // ---- S^T = K Q^T : two 32-key blocks ----
+    // The K operands are read kKWindow k-steps ahead of their MFMA; the
+    // sched_barriers keep the compiler from sinking each LDS read next to
+    // its use (which would expose the full LDS latency on every MFMA).
     f32x16 s[2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int i = 0; i < 16; ++i) s[kb][i] = 0.0f;
-#pragma unroll
-    for (int kk = 0; kk < KSTEPS; ++kk) {
-      const i16x8 a0 = *reinterpret_cast<const i16x8*>(kt + k_off[kk]);
-      const i16x8 a1 = *reinterpret_cast<const i16x8*>(kt + 32 * T::ROWB + k_off[kk]);
-      s[0] = Ops::mfma(a0, qf[kk], s[0]);
-      s[1] = Ops::mfma(a1, qf[kk], s[1]);
+    {
+      constexpr int KD = kKWindow;
+      i16x8 ka[KD][2];
+      static_for<0, KD>([&](auto i_c) {
+        constexpr int i = decltype(i_c)::value;
+        if constexpr (i < KSTEPS) {
+          ka[i][0] = *reinterpret_cast<const i16x8*>(kt + k_off[i]);
+          ka[i][1] = *reinterpret_cast<const i16x8*>(kt + 32 * T::ROWB + k_off[i]);
+        }
+      });
+      __builtin_amdgcn_sched_barrier(0);
+      static_for<0, KSTEPS>([&](auto kk_c) {
+        constexpr int kk = decltype(kk_c)::value;
+        s[0] = Ops::mfma(ka[kk % KD][0], qf[kk], s[0]);
+        s[1] = Ops::mfma(ka[kk % KD][1], qf[kk], s[1]);
+        if constexpr (kk + KD < KSTEPS) {
+          ka[kk % KD][0] = *reinterpret_cast<const i16x8*>(kt + k_off[kk + KD]);
+          ka[kk % KD][1] = *reinterpret_cast<const i16x8*>(kt + 32 * T::ROWB + k_off[kk + KD]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      });
     }
+    // Prefetch the first kVWindow V^T operands: their LDS latency hides
+    // behind the softmax.
+    constexpr int VD = kVWindow;
+    constexpr int NPV = DBLK * 4;
+    i16x8 va[VD];
+    static_for<0, VD>([&](auto i_c) {
+      constexpr int i = decltype(i_c)::value;
+      constexpr int db = i % DBLK, ch = i / DBLK;
+      constexpr int off = (2 + BUF) * T::BYTES + ch * 16 * T::ROWB;
+      va[i] = ds_read_tr_pair<off, off + 8 * T::ROWB>(v_addr[db]);
+    });
+    __builtin_amdgcn_sched_barrier(0);
 
     // ---- masking (ragged tail / causal diagonal) ----
     const bool need_mask = (kt0 + BN > N) || (CAUSAL && kt0 + BN - 1 > wrow0);
@@ -257,14 +296,13 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
     }
 
     // ---- online softmax with lazy rescale (reference online_softmax.cuh:89-152) ----
-    float mx = fmaxf(s[0][0], s[1][0]);
-#pragma unroll
-    for (int i = 1; i < 16; ++i) mx = fmaxf(mx, fmaxf(s[0][i], s[1][i]));
-    mx = pair_max(mx);
+    const float mx = pair_max(max32(s[0], s[1]));
     const bool grow = (mx - m_run) * c > kRescaleThreshold;  // false for NaN (-inf - -inf)
     if (__any(grow)) {
       const float m_new = grow ? mx : m_run;
-      const float alpha = grow ? fast_exp2((m_run - m_new) * c) : 1.0f;
+      // exp2(0) = 1 for rows that keep their max (branch-free: also covers
+      // m_run = -inf, where m_run - m_new would be NaN).
+      const float alpha = fast_exp2(grow ? (m_run - m_new) * c : 0.0f);
       m_run = m_new;
       neg_mc = -(m_run == -INFINITY ? 0.0f : m_run) * c;
       l_run0 *= alpha;
@@ -307,18 +345,26 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
     }
 
     // ---- O^T += V^T P^T ----
-#pragma unroll
-    for (int db = 0; db < DBLK; ++db) {
-      static_for<0, 4>([&](auto ch_c) {
-        constexpr int ch = decltype(ch_c)::value;
-        constexpr int off = (2 + BUF) * T::BYTES + ch * 16 * T::ROWB;
-        const i16x8 a = ds_read_tr_pair<off, off + 8 * T::ROWB>(v_addr[db]);
-        o_acc[db] = Ops::mfma(a, pf[ch], o_acc[db]);
-      });
-    }
+    // Raised wave priority while this wave issues its PV MFMAs: the other
+    // wave on the SIMD is then usually in its softmax (VALU), and the
+    // arbiter keeps the matrix pipe fed from this one.
+    __builtin_amdgcn_s_setprio(1);
+    __builtin_amdgcn_sched_barrier(0);
+    static_for<0, NPV>([&](auto j_c) {
+      constexpr int j = decltype(j_c)::value;
+      constexpr int db = j % DBLK, ch = j / DBLK;
+      o_acc[db] = Ops::mfma(va[j % VD], pf[ch], o_acc[db]);
+      if constexpr (j + VD < NPV) {
+        constexpr int db2 = (j + VD) % DBLK, ch2 = (j + VD) / DBLK;
+        constexpr int off = (2 + BUF) * T::BYTES + ch2 * 16 * T::ROWB;
+        va[j % VD] = ds_read_tr_pair<off, off + 8 * T::ROWB>(v_addr[db2]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    __builtin_amdgcn_s_setprio(0);
   };
 
-  auto tile_step = [&](auto buf_c, int t) {
+  auto tile_step = [&](auto buf_c, int t) FA_INLINE {
     constexpr int BUF = decltype(buf_c)::value;
     if (t + 1 < n_tiles) issue_tile(t + 1, BUF ^ 1);
     // Skip tiles whose every key lies after every row of this wave.

@@ -1,0 +1,103 @@
+"""ctypes binding of the C ABI declared in include/fa_mi355x.h.
+
+This is the binding a Python caller without the torch extension would write;
+the tests use it to load libfa_mi355x.so directly, check its exported
+symbols and validation branches on the CPU, and drive fa_fwd on the GPU with
+raw device pointers.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+REPO_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(REPO_ROOT, "include", "fa_mi355x.h")
+LIB_PATH = os.path.join(REPO_ROOT, "flash-attention_amd", "flash_attention_runtime",
+                        "libfa_mi355x.so")
+
+FA_OK, FA_ERR_NULL, FA_ERR_DTYPE, FA_ERR_SHAPE, FA_ERR_HEADDIM, FA_ERR_STRIDE, \
+    FA_ERR_UNSUPPORTED, FA_ERR_HIP, FA_ERR_ARG = range(9)
+FA_DTYPE_F16, FA_DTYPE_BF16 = 0, 1
+
+
+class FaFwdParams(ctypes.Structure):
+    _fields_ = [
+        ("q", ctypes.c_void_p),
+        ("k", ctypes.c_void_p),
+        ("v", ctypes.c_void_p),
+        ("o", ctypes.c_void_p),
+        ("lse", ctypes.POINTER(ctypes.c_float)),
+        ("q_stride", ctypes.c_int64 * 3),
+        ("k_stride", ctypes.c_int64 * 3),
+        ("v_stride", ctypes.c_int64 * 3),
+        ("o_stride", ctypes.c_int64 * 3),
+        ("batch", ctypes.c_int32),
+        ("heads", ctypes.c_int32),
+        ("seq_len", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("softmax_scale", ctypes.c_float),
+        ("causal", ctypes.c_int32),
+        ("dtype", ctypes.c_int32),
+    ]
+
+
+class FaDeviceInfo(ctypes.Structure):
+    _fields_ = [
+        ("name", ctypes.c_char * 256),
+        ("arch", ctypes.c_char * 64),
+        ("compute_units", ctypes.c_int32),
+        ("clock_khz", ctypes.c_int32),
+        ("lds_per_cu_bytes", ctypes.c_int64),
+        ("l2_bytes", ctypes.c_int64),
+        ("memory_bus_width_bits", ctypes.c_int32),
+        ("memory_clock_khz", ctypes.c_int32),
+        ("fp16_dense_peak_tflops", ctypes.c_double),
+        ("hbm_peak_gbps", ctypes.c_double),
+    ]
+
+
+def declared_functions(header: str = HEADER) -> list[str]:
+    """Names of the functions declared in the public header."""
+    text = open(header).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\**\s+\**(fa_\w+)\s*\(", text, re.M)))
+
+
+def load(path: str = LIB_PATH):
+    L = ctypes.CDLL(path)
+    P = ctypes.POINTER(FaFwdParams)
+    L.fa_fwd_validate.argtypes = [P]
+    L.fa_fwd_validate.restype = ctypes.c_int
+    L.fa_fwd.argtypes = [P, ctypes.c_void_p]
+    L.fa_fwd.restype = ctypes.c_int
+    L.fa_fwd_timed.argtypes = [P, ctypes.c_void_p, ctypes.POINTER(ctypes.c_float)]
+    L.fa_fwd_timed.restype = ctypes.c_int
+    L.fa_status_str.argtypes = [ctypes.c_int]
+    L.fa_status_str.restype = ctypes.c_char_p
+    L.fa_last_error.argtypes = []
+    L.fa_last_error.restype = ctypes.c_char_p
+    L.fa_device_info.argtypes = [ctypes.c_int, ctypes.POINTER(FaDeviceInfo)]
+    L.fa_device_info.restype = ctypes.c_int
+    L.fa_version.argtypes = []
+    L.fa_version.restype = ctypes.c_char_p
+    return L
+
+
+def params_from_tensors(q, k, v, o, lse=None, causal=False, scale=None):
+    """Fills FaFwdParams from torch tensors [B, H, N, D] (device pointers)."""
+    import math
+
+    import torch
+
+    p = FaFwdParams()
+    p.q, p.k, p.v, p.o = q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr()
+    p.lse = ctypes.cast(lse.data_ptr(), ctypes.POINTER(ctypes.c_float)) if lse is not None else None
+    for name, t in (("q_stride", q), ("k_stride", k), ("v_stride", v), ("o_stride", o)):
+        arr = getattr(p, name)
+        for i in range(3):
+            arr[i] = t.stride(i)
+    p.batch, p.heads, p.seq_len, p.head_dim = (int(x) for x in q.shape)
+    p.softmax_scale = 1.0 / math.sqrt(q.shape[3]) if scale is None else float(scale)
+    p.causal = 1 if causal else 0
+    p.dtype = FA_DTYPE_BF16 if q.dtype == torch.bfloat16 else FA_DTYPE_F16
+    return p
