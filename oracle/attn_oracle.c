@@ -42,6 +42,10 @@
  *      static reading; the emulator deliberately uses the mathematically
  *      correct Q.K^T, since the oracle is the mathematics.
  *
+ *  oracle_kernel_numerics_rows
+ *      The same emulation for selected (head, row) pairs only, so the 2x bar
+ *      can be checked on sampled rows of the full-size configs.
+ *
  *  oracle_round_f16 / oracle_round_bf16
  *      float -> IEEE binary16 / bfloat16 with round-to-nearest-even (the
  *      __float2half_rn / __float22half2_rn rounding the reference uses), plus
@@ -280,11 +284,46 @@ int oracle_ref_online_f32(const float* q, const float* k, const float* v, float*
 /* emulation of the reference kernel's numerics                             */
 /* ------------------------------------------------------------------------ */
 
+/* One query row i of head bh (q/k/v point at that head).  acc: D floats,
+ * s: block_n floats of scratch. */
+static void row_kernel_numerics(const float* qh, const float* kb, const float* vb, int N, int D,
+                                float scale, int causal, int dtype, int block_n, int i,
+                                float* acc, float* s, float* orow, float* lse) {
+  const float c = scale * 1.4426950408889634f; /* config.cuh:84 */
+  const float* qr = qh + (int64_t)i * D;
+  float m = -INFINITY, l = 0.0f;
+  for (int d = 0; d < D; ++d) acc[d] = 0.0f;
+  for (int t0 = 0; t0 < N; t0 += block_n) {
+    const int t1 = t0 + block_n < N ? t0 + block_n : N;
+    if (causal && t0 > i) break; /* fully masked tile: skipped */
+    float mt = m;
+    for (int j = t0; j < t1; ++j) {
+      float dot = 0.0f;
+      for (int d = 0; d < D; ++d) dot = fmaf(qr[d], kb[(int64_t)j * D + d], dot);
+      s[j - t0] = (causal && j > i) ? -INFINITY : dot;
+      mt = fmaxf(mt, s[j - t0]);
+    }
+    const float m_use = mt == -INFINITY ? 0.0f : mt;
+    const float alpha = exp2f((m - m_use) * c); /* online_softmax.cuh:17-19 */
+    l *= alpha;
+    for (int d = 0; d < D; ++d) acc[d] *= alpha;
+    for (int j = t0; j < t1; ++j) {
+      const float p = exp2f(s[j - t0] * c - m_use * c); /* :13-15 */
+      l += p;                                           /* unrounded p (:135-152) */
+      const float pr = round_to(p, dtype);              /* P -> fp16/bf16 RNE */
+      for (int d = 0; d < D; ++d) acc[d] = fmaf(pr, vb[(int64_t)j * D + d], acc[d]);
+    }
+    m = mt;
+  }
+  const float inv_l = 1.0f / l;
+  for (int d = 0; d < D; ++d) orow[d] = round_to(acc[d] * inv_l, dtype);
+  if (lse) *lse = (m == -INFINITY ? 0.0f : m) * scale + logf(l);
+}
+
 int oracle_kernel_numerics(const float* q, const float* k, const float* v, float* o, float* lse,
                            int B, int H, int N, int D, float scale, int causal, int dtype,
                            int block_n) {
   if (B < 1 || H < 1 || N < 1 || D < 1 || block_n < 1) return -1;
-  const float c = scale * 1.4426950408889634f; /* config.cuh:84 */
   int err = 0;
 #pragma omp parallel
   {
@@ -297,38 +336,40 @@ int oracle_kernel_numerics(const float* q, const float* k, const float* v, float
 #pragma omp for schedule(dynamic, 4) collapse(2)
       for (int bh = 0; bh < B * H; ++bh)
         for (int i = 0; i < N; ++i) {
-          const float* qr = q + ((int64_t)bh * N + i) * D;
-          const float* kb = k + (int64_t)bh * N * D;
-          const float* vb = v + (int64_t)bh * N * D;
-          float m = -INFINITY, l = 0.0f;
-          for (int d = 0; d < D; ++d) acc[d] = 0.0f;
-          for (int t0 = 0; t0 < N; t0 += block_n) {
-            const int t1 = t0 + block_n < N ? t0 + block_n : N;
-            if (causal && t0 > i) break; /* fully masked tile: skipped */
-            float mt = m;
-            for (int j = t0; j < t1; ++j) {
-              float dot = 0.0f;
-              for (int d = 0; d < D; ++d) dot = fmaf(qr[d], kb[(int64_t)j * D + d], dot);
-              s[j - t0] = (causal && j > i) ? -INFINITY : dot;
-              mt = fmaxf(mt, s[j - t0]);
-            }
-            const float m_use = mt == -INFINITY ? 0.0f : mt;
-            const float alpha = exp2f((m - m_use) * c); /* online_softmax.cuh:17-19 */
-            l *= alpha;
-            for (int d = 0; d < D; ++d) acc[d] *= alpha;
-            for (int j = t0; j < t1; ++j) {
-              const float p = exp2f(s[j - t0] * c - m_use * c); /* :13-15 */
-              l += p;                                           /* unrounded p (:135-152) */
-              const float pr = round_to(p, dtype);              /* P -> fp16/bf16 RNE */
-              for (int d = 0; d < D; ++d) acc[d] = fmaf(pr, vb[(int64_t)j * D + d], acc[d]);
-            }
-            m = mt;
-          }
-          const float inv_l = 1.0f / l;
-          float* orow = o + ((int64_t)bh * N + i) * D;
-          for (int d = 0; d < D; ++d) orow[d] = round_to(acc[d] * inv_l, dtype);
-          if (lse) lse[(int64_t)bh * N + i] = (m == -INFINITY ? 0.0f : m) * scale + logf(l);
+          const int64_t off = (int64_t)bh * N * D;
+          row_kernel_numerics(q + off, k + off, v + off, N, D, scale, causal, dtype, block_n, i,
+                              acc, s, o + off + (int64_t)i * D,
+                              lse ? lse + (int64_t)bh * N + i : NULL);
         }
+    }
+    free(acc);
+    free(s);
+  }
+  return err;
+}
+
+int oracle_kernel_numerics_rows(const float* q, const float* k, const float* v, int B, int H,
+                                int N, int D, float scale, int causal, int dtype, int block_n,
+                                const int32_t* sel_bh, const int32_t* sel_row, int64_t n_sel,
+                                float* o_sel, float* lse_sel) {
+  if (B < 1 || H < 1 || N < 1 || D < 1 || block_n < 1) return -1;
+  for (int64_t r = 0; r < n_sel; ++r)
+    if (sel_bh[r] < 0 || sel_bh[r] >= B * H || sel_row[r] < 0 || sel_row[r] >= N) return -2;
+  int err = 0;
+#pragma omp parallel
+  {
+    float* acc = (float*)malloc(sizeof(float) * (size_t)D);
+    float* s = (float*)malloc(sizeof(float) * (size_t)block_n);
+    if (!acc || !s) {
+#pragma omp atomic write
+      err = -3;
+    } else {
+#pragma omp for schedule(dynamic, 4)
+      for (int64_t r = 0; r < n_sel; ++r) {
+        const int64_t off = (int64_t)sel_bh[r] * N * D;
+        row_kernel_numerics(q + off, k + off, v + off, N, D, scale, causal, dtype, block_n,
+                            sel_row[r], acc, s, o_sel + r * D, lse_sel + r);
+      }
     }
     free(acc);
     free(s);

@@ -37,6 +37,10 @@ int oracle_kernel_numerics(const float* q, const float* k, const float* v, float
                            int B, int H, int N, int D, float scale, int causal, int dtype,
                            int block_n);
 
+int oracle_kernel_numerics_rows(const float* q, const float* k, const float* v, int B, int H,
+                                int N, int D, float scale, int causal, int dtype, int block_n,
+                                const int32_t* sel_bh, const int32_t* sel_row, int64_t n_sel,
+                                float* o_sel, float* lse_sel);
 void oracle_round_f16(const float* in, float* out, uint16_t* bits, int64_t n);
 void oracle_round_bf16(const float* in, float* out, uint16_t* bits, int64_t n);
 

@@ -64,12 +64,15 @@ def lib():
         L.oracle_ref_online_f32.argtypes = [fp, fp, fp, fp, i32, i32, i32, i32, f32, i32, i64, i64]
         L.oracle_kernel_numerics.argtypes = [fp, fp, fp, fp, fp, i32, i32, i32, i32, f32, i32,
                                              i32, i32]
+        L.oracle_kernel_numerics_rows.argtypes = [fp, fp, fp, i32, i32, i32, i32, f32, i32, i32,
+                                                  i32, ip, ip, i64, fp, fp]
         L.oracle_round_f16.argtypes = [fp, fp, up, i64]
         L.oracle_round_bf16.argtypes = [fp, fp, up, i64]
         L.oracle_num_threads.argtypes = []
         L.oracle_set_num_threads.argtypes = [i32]
         for name in ("oracle_attn_f64", "oracle_attn_rows_f64", "oracle_ref_online_f32",
-                     "oracle_kernel_numerics", "oracle_num_threads"):
+                     "oracle_kernel_numerics", "oracle_kernel_numerics_rows",
+                     "oracle_num_threads"):
             getattr(L, name).restype = ctypes.c_int
         _lib = L
     return _lib
@@ -162,6 +165,30 @@ def kernel_numerics(q, k, v, scale, causal=False, dtype=F16, block_n=64):
                                       int(block_n))
     if rc != 0:
         raise RuntimeError(f"oracle_kernel_numerics failed: {rc}")
+    return o, lse
+
+
+def kernel_numerics_rows(q, k, v, scale, causal, sel_bh, sel_row, dtype=F16, block_n=64):
+    """kernel_numerics for selected rows (flattened head bh = b*H + h, query
+    row i).  Returns (o [n_sel, D] f32, lse [n_sel] f32)."""
+    _check_qkv(q, k, v)
+    B, H, N, D = q.shape
+    q, qp = _f32(q)
+    k, kp = _f32(k)
+    v, vp = _f32(v)
+    sel_bh = np.ascontiguousarray(sel_bh, dtype=np.int32)
+    sel_row = np.ascontiguousarray(sel_row, dtype=np.int32)
+    n = sel_bh.size
+    o = np.empty((n, D), np.float32)
+    lse = np.empty((n,), np.float32)
+    ip = ctypes.POINTER(ctypes.c_int32)
+    fpp = ctypes.POINTER(ctypes.c_float)
+    rc = lib().oracle_kernel_numerics_rows(qp, kp, vp, B, H, N, D, float(scale),
+                                           int(bool(causal)), int(dtype), int(block_n),
+                                           sel_bh.ctypes.data_as(ip), sel_row.ctypes.data_as(ip),
+                                           n, o.ctypes.data_as(fpp), lse.ctypes.data_as(fpp))
+    if rc != 0:
+        raise RuntimeError(f"oracle_kernel_numerics_rows failed: {rc}")
     return o, lse
 
 

@@ -115,11 +115,17 @@ def test_config_sampled_rows_vs_oracle(fa, oracle, name):
                                            torch.tensor(sel_row, device=DEV).long()])
     got_lse = to_np32(lse.reshape(B * H, N)[torch.tensor(sel_bh, device=DEV).long(),
                                             torch.tensor(sel_row, device=DEV).long()])
+    emu_o, _ = oracle.kernel_numerics_rows(qn, kn, vn, scale, causal, local_bh, sel_row,
+                                           oracle.BF16 if dtype == "bf16" else oracle.F16)
     mx, mean = err_stats(got_o, ref_o)
+    emx, emean = err_stats(emu_o, ref_o)
     lse_err = float(np.abs(got_lse.astype(np.float64) - ref_lse).max())
-    _note(f"  sampled {len(sel_row)} rows: max_abs={mx:.3e} mean_abs={mean:.3e} lse={lse_err:.3e}")
+    _note(f"  sampled {len(sel_row)} rows: max_abs={mx:.3e} mean_abs={mean:.3e} "
+          f"(ref-kernel emu {emx:.3e}/{emean:.3e}) lse={lse_err:.3e}")
     assert mx <= MAX_ABS_TOL
     assert mean <= MEAN_ABS_TOL
+    assert mx <= 2 * emx + 1e-6, f"max-abs {mx} > 2x reference-kernel error {emx}"
+    assert mean <= 2 * emean + 1e-6, f"mean-abs {mean} > 2x reference-kernel error {emean}"
     assert lse_err <= LSE_TOL
 
     # Every O row is a convex combination of the visible V rows: per head dim,

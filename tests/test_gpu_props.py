@@ -1,0 +1,82 @@
+"""Size-independent properties of the HIP forward at the full BASELINE sizes,
+and HIP-graph capture of the product entry point.
+
+These complement the oracle comparisons in test_gpu_parity.py at sizes where
+the fp64 oracle cannot cover every row:
+  * homogeneity in V: P does not depend on V and every step of P.V, the
+    normalisation and the RNE output rounding commutes with a power-of-two
+    scale, so O(q, k, 2v) == 2 O(q, k, v) bit for bit and LSE is unchanged;
+  * V constant: every O row is a convex combination of the V rows, so O == c;
+  * a captured HIP graph replays to the eager result, several times, with
+    eager work in between.
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from helpers import CONFIGS, MAX_ABS_TOL, MEAN_ABS_TOL, make_config
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def _note(msg):
+    print(msg, flush=True)
+
+
+@pytest.mark.parametrize("name", ["C2", "C3", "C4", "C5r"])
+def test_v_power_of_two_homogeneity(fa, name):
+    _note(f"case V*2 homogeneity {name}")
+    q, k, v, causal, scale = make_config(name, device=DEV)
+    o1, l1 = fa.forward(q, k, v, causal=causal, return_lse=True)
+    o2, l2 = fa.forward(q, k, v * 2, causal=causal, return_lse=True)
+    torch.cuda.synchronize()
+    assert torch.equal(o2, o1 * 2)
+    assert torch.equal(l1, l2)
+
+
+@pytest.mark.parametrize("name", ["C2", "C4", "C5r"])
+def test_v_constant_gives_constant_output(fa, name):
+    _note(f"case V=const {name}")
+    q, k, v, causal, scale = make_config(name, device=DEV)
+    c = 1.375
+    vc = torch.full_like(v, c)
+    o = fa.forward(q, k, vc, causal=causal)
+    torch.cuda.synchronize()
+    d = (o.float() - c).abs()
+    _note(f"  max_abs={d.max().item():.3e} mean_abs={d.mean().item():.3e}")
+    assert d.max().item() <= MAX_ABS_TOL
+    assert d.mean().item() <= MEAN_ABS_TOL
+    if CONFIGS[name][4] == "fp16":
+        # fp16 normalises by the sum of the rounded P that enters P.V: exact.
+        assert d.max().item() == 0.0
+
+
+@pytest.mark.parametrize("name", ["C2", "C5r"])
+def test_hip_graph_replay_matches_eager(fa, name):
+    _note(f"case HIP graph capture {name}")
+    q, k, v, causal, scale = make_config(name, device=DEV)
+    ref = fa.forward(q, k, v, causal=causal)
+    o = torch.empty_like(q)
+    # Warm up on a side stream (torch's capture protocol), then capture.
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fa.forward(q, k, v, o, causal=causal)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = fa.forward(q, k, v, o, causal=causal)
+    assert out.data_ptr() == o.data_ptr()
+    for rep in range(4):
+        o.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(o, ref), f"replay {rep}"
+        # eager work between replays
+        e = fa.forward(q, k, v, causal=causal)
+        torch.cuda.synchronize()
+        assert torch.equal(e, ref)

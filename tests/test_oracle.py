@@ -125,6 +125,19 @@ def test_kernel_numerics_emulator(oracle, dtype, causal):
     assert np.abs(el - lse).max() <= 1e-4
 
 
+@pytest.mark.parametrize("causal", [False, True])
+def test_kernel_numerics_rows_matches_full(oracle, causal):
+    """The row-selective emulator is the full emulator restricted to the
+    selected rows, bit for bit."""
+    q, k, v = _rand_inputs((2, 2, 150, 64), seed=9)
+    eo, el = oracle.kernel_numerics(q, k, v, 0.125, causal, oracle.F16)
+    sel_bh = np.array([0, 3, 1, 2, 3], np.int32)
+    sel_row = np.array([0, 149, 64, 63, 100], np.int32)
+    ro, rl = oracle.kernel_numerics_rows(q, k, v, 0.125, causal, sel_bh, sel_row, oracle.F16)
+    assert np.array_equal(ro, eo.reshape(4, 150, 64)[sel_bh, sel_row])
+    assert np.array_equal(rl, el.reshape(4, 150)[sel_bh, sel_row])
+
+
 def test_round_f16_matches_numpy(oracle):
     rng = np.random.default_rng(0)
     x = np.concatenate([
