@@ -29,7 +29,7 @@ import sys
 import time
 
 REPO_ROOT = os.path.dirname(os.path.abspath(__file__))
-sys.path.insert(0, os.path.join(REPO_ROOT, "flash-attention_amd"))
+sys.path.insert(0, os.path.join(REPO_ROOT, "flash-attention_amd"))  # runtime + fa_bench
 sys.path.insert(0, REPO_ROOT)
 
 PEAK_FP16_TFLOPS = 2500.0  # MI355X published dense fp16/bf16 MFMA peak
@@ -51,22 +51,19 @@ def flops(B, H, N, D, causal):
     return f / 2 if causal else f
 
 
-def make_inputs(torch, name, device):
+def make_inputs(torch, name, device, input_mode="random"):
+    from fa_bench.input_data import generate_qkv
+
     B, H, N, D, dtype, causal, sigma, case = WORKLOADS[name]
-    gen = torch.Generator(device=device)
-    gen.manual_seed(1234 + 100003 * case)
     td = {"fp16": torch.float16, "bf16": torch.bfloat16}[dtype]
-    qkv = []
-    for i in range(3):
-        t = torch.randn((B, H, N, D), generator=gen, device=device, dtype=torch.float32)
-        if i < 2 and sigma != 1.0:
-            t = t * sigma
-        qkv.append(t.to(td))
-    return qkv, causal
+    q, k, v, _ = generate_qkv(batch_size=B, n_heads=H, seq_len=N, d_head=D, dtype=td,
+                              device=device, input_mode=input_mode, seed=1234, case_index=case,
+                              qk_sigma=sigma)
+    return (q, k, v), causal
 
 
-def time_workload(torch, fa, name, steps, warmup):
-    (q, k, v), causal = make_inputs(torch, name, "cuda")
+def time_workload(torch, fa, name, steps, warmup, input_mode="random"):
+    (q, k, v), causal = make_inputs(torch, name, "cuda", input_mode)
     o = torch.empty_like(q)
     for _ in range(warmup):
         fa.forward(q, k, v, o, causal=causal)
@@ -85,6 +82,42 @@ def time_workload(torch, fa, name, steps, warmup):
     B, H, N, D = q.shape
     tflops = flops(B, H, N, D, causal) / (ms * 1e-3) / 1e12
     return ms, tflops, wall_ms
+
+
+def gemm_ceiling(torch, steps, warmup):
+    """Times square torch.matmul GEMMs (hipBLASLt on ROCm) on N(0,1) and on
+    constant operands.  MI355X clocks depend on the data the matrix cores
+    toggle, so the random-data figure is the relevant ceiling for attention
+    on random inputs.  Prints one JSON line per case."""
+    for dt_name, dt in (("fp16", torch.float16), ("bf16", torch.bfloat16)):
+        for n in (8192, 16384):
+            for data in ("randn", "ones"):
+                g = torch.Generator(device="cuda")
+                g.manual_seed(7)
+                if data == "randn":
+                    a = torch.randn((n, n), generator=g, device="cuda").to(dt)
+                    b = torch.randn((n, n), generator=g, device="cuda").to(dt)
+                else:
+                    a = torch.ones((n, n), device="cuda", dtype=dt)
+                    b = torch.ones((n, n), device="cuda", dtype=dt)
+                c = torch.empty((n, n), device="cuda", dtype=dt)
+                for _ in range(max(warmup, 3)):
+                    torch.matmul(a, b, out=c)
+                reps = max(5, min(steps, 50))
+                start = torch.cuda.Event(enable_timing=True)
+                stop = torch.cuda.Event(enable_timing=True)
+                torch.cuda.synchronize()
+                start.record()
+                for _ in range(reps):
+                    torch.matmul(a, b, out=c)
+                stop.record()
+                torch.cuda.synchronize()
+                ms = start.elapsed_time(stop) / reps
+                print(json.dumps({"gemm": f"{n}x{n}x{n}", "dtype": dt_name, "data": data,
+                                  "ms": round(ms, 4),
+                                  "tflops": round(2.0 * n ** 3 / (ms * 1e-3) / 1e12, 1)}),
+                      flush=True)
+                del a, b, c
 
 
 def cpu_baseline(name, budget_s=12.0):
@@ -146,6 +179,11 @@ def main():
     ap.add_argument("--workload", default="C3", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--all", action="store_true", help="also time every config (stderr table)")
+    ap.add_argument("--input-mode", default="random", choices=["random", "structured", "stress"],
+                    help="input values (the headline metric is quoted on random)")
+    ap.add_argument("--gemm-ceiling", action="store_true",
+                    help="instead of attention, time torch.matmul (hipBLASLt) fp16/bf16 GEMMs on "
+                         "N(0,1) and on constant data: the data-dependent MFMA ceiling of the box")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="instead of attention, time a plain device copy of this many MiB "
                          "(calibrates the FETCH_SIZE / WRITE_SIZE counters)")
@@ -184,9 +222,13 @@ def main():
                           "GBps_read_plus_write": 2 * n * 4 / (ms * 1e-3) / 1e9}), flush=True)
         return
 
+    if args.gemm_ceiling:
+        gemm_ceiling(torch, args.steps, args.warmup)
+        return
+
     name = args.workload
     B, H, N, D, dtype, causal, sigma, case = WORKLOADS[name]
-    ms, tflops, wall_ms = time_workload(torch, fa, name, args.steps, args.warmup)
+    ms, tflops, wall_ms = time_workload(torch, fa, name, args.steps, args.warmup, args.input_mode)
     info = fa.device_info(0)
 
     traffic = None
@@ -197,7 +239,8 @@ def main():
     if args.all:
         print(f"{'cfg':5s} {'ms':>9s} {'TFLOPS':>9s} {'%peak':>7s}", file=sys.stderr)
         for wn in WORKLOADS:
-            wms, wtf, _ = time_workload(torch, fa, wn, max(10, args.steps // 2), args.warmup)
+            wms, wtf, _ = time_workload(torch, fa, wn, max(10, args.steps // 2), args.warmup,
+                                        args.input_mode)
             print(f"{wn:5s} {wms:9.4f} {wtf:9.1f} {100 * wtf / PEAK_FP16_TFLOPS:6.1f}%",
                   file=sys.stderr, flush=True)
 
@@ -215,7 +258,8 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": dtype,
-        "data": "synthetic: Q,K,V ~ N(0,1) seeded (input_data.py random mode), resident in HBM",
+        "data": (f"synthetic, resident in HBM: {args.input_mode} mode"
+                 + (" (Q,K,V ~ N(0,1), seed 1234 + 100003*case)" if args.input_mode == "random" else "")),
         "config": {
             "workload": f"{name}: B={B} H={H} N={N} D={D} {dtype} "
                         f"{'causal' if causal else 'non-causal'} FA2 forward",

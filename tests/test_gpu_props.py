@@ -5,7 +5,9 @@ These complement the oracle comparisons in test_gpu_parity.py at sizes where
 the fp64 oracle cannot cover every row:
   * homogeneity in V: P does not depend on V and every step of P.V, the
     normalisation and the RNE output rounding commutes with a power-of-two
-    scale, so O(q, k, 2v) == 2 O(q, k, v) bit for bit and LSE is unchanged;
+    scale, so O(q, k, 2v) == 2 O(q, k, v) bit for bit wherever O is a normal
+    number (subnormal fp16 outputs may differ by one 2^-24 step) and LSE is
+    unchanged;
   * V constant: every O row is a convex combination of the V rows, so O == c;
   * a captured HIP graph replays to the eager result, several times, with
     eager work in between.
@@ -33,8 +35,23 @@ def test_v_power_of_two_homogeneity(fa, name):
     o1, l1 = fa.forward(q, k, v, causal=causal, return_lse=True)
     o2, l2 = fa.forward(q, k, v * 2, causal=causal, return_lse=True)
     torch.cuda.synchronize()
-    assert torch.equal(o2, o1 * 2)
     assert torch.equal(l1, l2)
+    # Exact wherever O is a normal number of the output type.  fp16 outputs
+    # below 2^-14 are subnormal: their rounding step is a fixed 2^-24, so
+    # round(2x) and 2 round(x) may differ by that one step.
+    # An output equal to 2^-14 may itself be a rounded-up subnormal.
+    tiny = torch.finfo(o1.dtype).tiny
+    normal = o1.abs() > tiny
+    diff = (o2.float() - 2 * o1.float()).abs()
+    bad = normal & (diff != 0)
+    n_bad = int(bad.sum().item())
+    if n_bad:
+        _note(f"  mismatching o1 values: {o1[bad][:8].tolist()} o2: {o2[bad][:8].tolist()}")
+    sub_max = diff[~normal].max().item() if (~normal).any() else 0.0
+    _note(f"  normal mismatches={n_bad} subnormal outputs={int((~normal).sum().item())} "
+          f"subnormal max diff={sub_max:.3e}")
+    assert n_bad == 0
+    assert sub_max <= 2.0 ** -24
 
 
 @pytest.mark.parametrize("name", ["C2", "C4", "C5r"])
