@@ -3,6 +3,7 @@
 Outputs (next to the Python package, so they travel with the repository):
   flash_attention_runtime/libfa_mi355x.so   HIP kernels + C ABI (hipcc, gfx950)
   flash_attention_runtime/_C<EXT_SUFFIX>     torch/pybind binding over the C ABI
+  flash_attention_runtime/fa_profile         C++ benchmark CLI over the C ABI
 
 Replaces the reference's JIT build (python/flash_attention_runtime/
 __init__.py:10-27, torch.utils.cpp_extension.load of _ext.cu with nvcc) by an
@@ -112,10 +113,22 @@ def build_torch_binding() -> str:
     return out
 
 
+def build_profile_cli() -> str:
+    """Links the fa_profile executable (csrc/fa_profile.cpp) against
+    libfa_mi355x.so (rpath $ORIGIN)."""
+    out = os.path.join(OUT_DIR, "fa_profile")
+    _run([_hipcc(), "-O2", "-std=c++17", "-Wall", "-I", INCLUDE,
+          os.path.join(CSRC, "fa_profile.cpp"), f"-L{OUT_DIR}", "-lfa_mi355x",
+          "-Wl,-rpath,$ORIGIN", "-o", out + ".tmp"])
+    os.replace(out + ".tmp", out)
+    return out
+
+
 def build(jobs: int = 8) -> list[str]:
     lib = build_hip_library(jobs)
     ext = build_torch_binding()
-    return [lib, ext]
+    cli = build_profile_cli()
+    return [lib, ext, cli]
 
 
 def main() -> None:

@@ -1,0 +1,49 @@
+"""The benchmark harness on the GPU: the pybind benchmark CLI
+(fa_bench/benchmark_pybind.py) and the C++ fa_profile executable, at small
+shapes, produce well-formed rows in the reference's formats."""
+from __future__ import annotations
+
+import os
+import subprocess
+
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+PROFILE = os.path.join(REPO, "flash-attention_amd", "flash_attention_runtime", "fa_profile")
+
+
+def test_benchmark_pybind_rows(tmp_path, capsys):
+    from fa_bench.benchmark_pybind import main
+    from fa_bench.schema import CSV_COLUMNS
+
+    print("case benchmark_pybind small", flush=True)
+    out_csv = tmp_path / "r.csv"
+    rows = main(["--d_heads", "64,128", "--seq_lens", "256", "--batch_size", "1", "--n_heads",
+                 "2", "--warmups", "1", "--repeats", "3", "--csv", "--out_csv", str(out_csv),
+                 "--result_json", str(tmp_path / "result.json")])
+    kernels = {r["kernel"] for r in rows}
+    assert "fa2_pybind" in kernels
+    assert len([r for r in rows if r["kernel"] == "fa2_pybind"]) == 2
+    for r in rows:
+        assert float(r["mean_ms"]) > 0 and float(r["attn_tflops"]) > 0
+    lines = out_csv.read_text().strip().splitlines()
+    assert lines[0] == ",".join(CSV_COLUMNS)
+    assert len(lines) == 1 + len(rows)
+    assert all(len(ln.split(",")) == 30 for ln in lines)
+    assert (tmp_path / "result.json").exists()
+
+
+@pytest.mark.parametrize("extra", [[], ["--dtype", "bf16", "--causal"]])
+def test_fa_profile_csv_line(extra):
+    print(f"case fa_profile {extra}", flush=True)
+    r = subprocess.run([PROFILE, "2x2x300x64", "--warmup-iters", "1", "--benchmark-iters", "3",
+                        *extra], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    csv = [ln for ln in r.stdout.splitlines() if ln.startswith("CSV,")]
+    assert len(csv) == 1
+    f = csv[0].split(",")
+    assert len(f) == 13
+    assert f[1:5] == ["2", "2", "300", "64"]
+    assert float(f[5]) > 0 and float(f[6]) > 0
