@@ -99,6 +99,9 @@ constexpr float kRescaleThreshold = 8.0f;
 constexpr int kKWindow = 3;
 constexpr int kVWindow = 4;
 
+// Non-causal problems with at least this many keys use 8-wave workgroups.
+constexpr int kWideMinSeq = 2048;
+
 template <int D, bool BF16, bool CAUSAL, int NW>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
     fa_fwd_kernel(const KernelArgs args) {
@@ -415,8 +418,14 @@ hipError_t launch_one(const KernelArgs& a, hipStream_t stream) {
 
 template <int D, bool BF16>
 hipError_t launch_causal(const KernelArgs& a, hipStream_t stream) {
-  return a.causal ? launch_one<D, BF16, true, 4>(a, stream)
-                  : launch_one<D, BF16, false, 4>(a, stream);
+  if (a.causal) return launch_one<D, BF16, true, 4>(a, stream);
+  // Long non-causal rows: 8 waves (BM = 256) per workgroup, one workgroup
+  // per CU, halve the L2->LDS tile traffic per flop; the chip is power
+  // limited there and the saved data movement buys clock (measured +3 % at
+  // N = 4096).  Shorter or causal problems keep 4 waves and two workgroups
+  // per CU, which fill the machine better.
+  if (a.seq_len >= kWideMinSeq) return launch_one<D, BF16, false, 8>(a, stream);
+  return launch_one<D, BF16, false, 4>(a, stream);
 }
 
 }  // namespace

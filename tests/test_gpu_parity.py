@@ -69,6 +69,19 @@ def test_small_shapes_vs_oracle(fa, oracle, N, D, dtype, causal):
     _check_against_oracle(oracle, q, k, v, o, lse, causal, scale, dtype)
 
 
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("N", [2048, 2049, 2300])
+def test_wide_workgroup_shapes_vs_oracle(fa, oracle, N, D, dtype):
+    """Non-causal N >= 2048 runs on the 8-wave (256-row) workgroup variant:
+    every row against the oracle, including a ragged tail."""
+    _note(f"case wide N={N} D={D} {dtype}")
+    q, k, v = make_qkv(1, 2, N, D, dtype, seed=case_seed(N * 13 + D), device="cpu")
+    scale = 1.0 / math.sqrt(D)
+    o, lse = _fwd(fa, q.to(DEV), k.to(DEV), v.to(DEV), False)
+    _check_against_oracle(oracle, q, k, v, o, lse, False, scale, dtype)
+
+
 def test_config_c1_full_vs_oracle(fa, oracle):
     """C1 (the reference's CPU-runnable case) end to end, every row."""
     q, k, v, causal, scale = make_config("C1")
