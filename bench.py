@@ -120,7 +120,7 @@ def gemm_ceiling(torch, steps, warmup):
                 del a, b, c
 
 
-def cpu_baseline(name, budget_s=12.0):
+def cpu_baseline(name, budget_s=15.0):
     """Times the reference CPU path (oracle_ref_online_f32: fp32 online softmax
     with expf, one query row at a time) on the first rows of the workload, on
     all host threads OpenMP gives it; returns TFLOP/s of the same metric."""
