@@ -35,6 +35,8 @@ fa_status fail(fa_status s, const char* fmt, ...) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+constexpr int64_t kMaxSeqStride = int64_t(1) << 24;
+
 // Checks one tensor's strides.  The kernels read rows with 16-byte vector
 // loads, so every row start must be 16-byte aligned: the base pointer and all
 // three strides (in 2-byte elements) must be multiples of 8 elements.  The
@@ -53,6 +55,11 @@ fa_status check_strides(const char* name, const void* ptr, const int64_t st[3], 
   if (st[2] < head_dim && seq_len > 1)
     return fail(FA_ERR_STRIDE, "%s seq stride %lld is smaller than head_dim %lld (rows overlap)",
                 name, (long long)st[2], (long long)head_dim);
+  // K/V tiles are staged with 32-bit byte offsets from the tile's first row
+  // (up to 63 rows of 2*stride bytes), which bounds the seq stride.
+  if (st[2] > kMaxSeqStride)
+    return fail(FA_ERR_UNSUPPORTED, "%s seq stride %lld exceeds %lld elements", name,
+                (long long)st[2], (long long)kMaxSeqStride);
   if (!aligned16(ptr)) return fail(FA_ERR_STRIDE, "%s pointer is not 16-byte aligned", name);
   return FA_OK;
 }

@@ -24,8 +24,9 @@
  *   mask_ij = -inf when causal and j > i (top-left aligned), else 0.
  * Tensors are [batch, heads, seq_len, head_dim] with unit stride along
  * head_dim; the batch/head/seq strides are free (so BNHD views work without a
- * copy).  O has the input dtype; LSE is fp32 [batch, heads, seq_len],
- * contiguous, and optional.
+ * copy) up to a seq stride of 2^24 elements (FA_ERR_UNSUPPORTED beyond).
+ * O has the input dtype; LSE is fp32 [batch, heads, seq_len], contiguous,
+ * and optional.
  *
  * Ownership: all pointers are borrowed; the library allocates no device memory.
  * Threading: re-entrant; the only mutable global state is a thread-local error

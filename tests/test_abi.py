@@ -257,6 +257,14 @@ def test_misaligned_lse(lib):
     check(lib, p, A.FA_ERR_STRIDE, "lse")
 
 
+def test_seq_stride_limit(lib):
+    p = contiguous(N=16, D=64)
+    p.v_stride[2] = 1 << 24
+    check(lib, p, A.FA_OK)
+    p.v_stride[2] = (1 << 24) + 8
+    check(lib, p, A.FA_ERR_UNSUPPORTED, "v seq stride")
+
+
 def test_grid_limit(lib):
     ok = contiguous(B=1 << 15, H=1 << 15, N=128, D=64)  # 2^30 workgroups
     check(lib, ok, A.FA_OK)

@@ -82,6 +82,28 @@ def test_wide_workgroup_shapes_vs_oracle(fa, oracle, N, D, dtype):
     _check_against_oracle(oracle, q, k, v, o, lse, False, scale, dtype)
 
 
+@pytest.mark.parametrize("causal", [False, True], ids=["noncausal", "causal"])
+@pytest.mark.parametrize("D", [64, 128])
+def test_strided_bnhd_views(fa, oracle, D, causal):
+    """Q, K, V and O given as [B, H, N, D] views of [B, N, H, D] storage
+    (the layout input_data.py:81-87 permutes away with a copy) run without a
+    copy and give bit-identical results to contiguous inputs."""
+    _note(f"case strided BNHD D={D} causal={causal}")
+    B, H, N = 2, 3, 300
+    q, k, v = make_qkv(B, H, N, D, "fp16", seed=case_seed(77 + D), device="cpu")
+    qs, ks, vs = (t.permute(0, 2, 1, 3).contiguous().to(DEV).permute(0, 2, 1, 3) for t in (q, k, v))
+    assert not qs.is_contiguous() and qs.stride(1) == D
+    o_store = torch.empty(B, N, H, D, device=DEV, dtype=torch.float16)
+    o_view = o_store.permute(0, 2, 1, 3)
+    out, lse = fa.forward(qs, ks, vs, o_view, causal=causal, return_lse=True)
+    torch.cuda.synchronize()
+    assert out.data_ptr() == o_store.data_ptr()
+    ref_o, ref_lse = _fwd(fa, q.to(DEV), k.to(DEV), v.to(DEV), causal)
+    assert torch.equal(o_view, ref_o)
+    assert torch.equal(lse, ref_lse)
+    _check_against_oracle(oracle, q, k, v, o_view, lse, causal, 1.0 / math.sqrt(D), "fp16")
+
+
 def test_config_c1_full_vs_oracle(fa, oracle):
     """C1 (the reference's CPU-runnable case) end to end, every row."""
     q, k, v, causal, scale = make_config("C1")
