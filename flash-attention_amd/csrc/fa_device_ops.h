@@ -108,11 +108,6 @@ __device__ __forceinline__ void pair_values(float x, float& lo, float& hi) {
   lo = __builtin_bit_cast(float, a);
   hi = __builtin_bit_cast(float, b);
 }
-__device__ __forceinline__ float pair_max(float x) {
-  float lo, hi;
-  pair_values(x, lo, hi);
-  return fmaxf(lo, hi);
-}
 // max(a, b, c) in one v_max3_f32.  Issued from inline asm because fmaxf
 // makes the compiler quiet possible signalling NaNs with an extra v_max of
 // each MFMA result first; the scores here are never NaN.
@@ -120,6 +115,13 @@ __device__ __forceinline__ float max3(float a, float b, float c) {
   float d;
   asm("v_max3_f32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
   return d;
+}
+// Max over lanes l and l^32 (v_max3 with a repeated operand: no
+// canonicalising v_max of the inputs, which fmaxf would add).
+__device__ __forceinline__ float pair_max(float x) {
+  float lo, hi;
+  pair_values(x, lo, hi);
+  return max3(lo, hi, hi);
 }
 
 // Max of the 32 values of two MFMA accumulators: a v_max3 tree of depth 4
