@@ -178,6 +178,30 @@ def test_config_sampled_rows_vs_oracle(fa, oracle, name):
     assert bool((of >= vmin - margin).all().item()), "O below the convex hull of V"
 
 
+@pytest.mark.parametrize("causal", [False, True], ids=["noncausal", "causal"])
+def test_long_sequence_sampled_rows(fa, oracle, causal):
+    """N = 32768 (beyond every BASELINE config): sampled rows against the
+    oracle, the tail rows included, to guard the index arithmetic."""
+    B, H, N, D = 1, 2, 32768, 128
+    _note(f"case long N={N} causal={causal}")
+    q, k, v = make_qkv(B, H, N, D, "fp16", seed=case_seed(9), device=DEV)
+    scale = 1.0 / math.sqrt(D)
+    o, lse = _fwd(fa, q, k, v, causal)
+    rows = np.array([0, 1, 255, 256, 4095, 16384, 32511, N - 2, N - 1], np.int32)
+    sel_bh = np.repeat(np.arange(B * H, dtype=np.int32), rows.size)
+    sel_row = np.tile(rows, B * H)
+    qn, kn, vn = to_np32(q), to_np32(k), to_np32(v)
+    ref_o, ref_lse = oracle.attn_rows_f64(qn, kn, vn, scale, causal, sel_bh, sel_row)
+    got_o = to_np32(o.reshape(B * H, N, D)[torch.tensor(sel_bh).long().to(DEV),
+                                           torch.tensor(sel_row).long().to(DEV)])
+    got_lse = to_np32(lse.reshape(B * H, N)[torch.tensor(sel_bh).long().to(DEV),
+                                            torch.tensor(sel_row).long().to(DEV)])
+    mx, mean = err_stats(got_o, ref_o)
+    lse_err = float(np.abs(got_lse.astype(np.float64) - ref_lse).max())
+    _note(f"  max_abs={mx:.3e} mean_abs={mean:.3e} lse={lse_err:.3e}")
+    assert mx <= MAX_ABS_TOL and mean <= MEAN_ABS_TOL and lse_err <= LSE_TOL
+
+
 @pytest.mark.parametrize("name", ["C2", "C3", "C4", "C5r"])
 def test_config_zero_query_closed_form(fa, name):
     """Q = 0 makes every visible score 0: O_i = mean of the visible V rows
