@@ -185,3 +185,23 @@ extern "C" int kat_dma(int* out) {
   if (dout) (void)hipFree(dout);
   return rc;
 }
+
+__global__ void kat_xcd_kernel(int total, int* out) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b < total) out[b] = fa::dev::xcd_remap(b, total);
+}
+
+// out[b] = xcd_remap(b, total) for every dispatch index b < total.
+extern "C" int kat_xcd_remap(int total, int* out) {
+  if (total < 1) return -1;
+  void* d = 0;
+  int rc = check(hipMalloc(&d, (size_t)total * 4));
+  if (!rc) {
+    hipLaunchKernelGGL(kat_xcd_kernel, dim3((total + 255) / 256), dim3(256), 0, 0, total, (int*)d);
+    rc = check(hipGetLastError());
+  }
+  if (!rc) rc = check(hipDeviceSynchronize());
+  if (!rc) rc = check(hipMemcpy(out, d, (size_t)total * 4, hipMemcpyDeviceToHost));
+  if (d) (void)hipFree(d);
+  return rc;
+}

@@ -26,6 +26,7 @@ def kat():
     L.kat_pack2.argtypes = [ctypes.c_int, fp, ctypes.POINTER(ctypes.c_uint32), fp]
     L.kat_pair.argtypes = [fp, fp, fp]
     L.kat_dma.argtypes = [ctypes.POINTER(ctypes.c_int32)]
+    L.kat_xcd_remap.argtypes = [ctypes.c_int, ctypes.POINTER(ctypes.c_int32)]
     return L
 
 
@@ -165,3 +166,24 @@ def test_dma_lane_placement(kat):
     src_chunk = (lanes * 7) % 64
     expect = (src_chunk[:, None] * 4 + np.arange(4)[None, :]).reshape(-1)
     assert np.array_equal(out[256:], expect)
+
+
+@pytest.mark.parametrize("total", [1, 5, 8, 9, 15, 16, 17, 100, 2048, 4097, 12345])
+def test_xcd_remap_is_contiguous_per_xcd(kat, total):
+    """xcd_remap is a permutation of [0, total) under which the dispatch
+    indices the hardware sends to XCD x (b % 8 == x) own one contiguous
+    logical range, the ranges ascending with x."""
+    print(f"case xcd_remap total={total}", flush=True)
+    out = np.zeros(total, np.int32)
+    assert kat.kat_xcd_remap(total, out.ctypes.data_as(ctypes.POINTER(ctypes.c_int32))) == 0
+    assert np.array_equal(np.sort(out), np.arange(total))
+    prev_hi = -1
+    for x in range(8):
+        ids = np.sort(out[np.arange(total) % 8 == x])
+        if ids.size == 0:
+            continue
+        assert np.array_equal(ids, np.arange(ids[0], ids[0] + ids.size)), x
+        assert ids[0] == prev_hi + 1
+        prev_hi = ids[-1]
+        # consecutive dispatches on one XCD walk its range in order
+        assert np.all(np.diff(out[np.arange(total) % 8 == x]) == 1)
