@@ -36,20 +36,37 @@ def _fwd(fa, q, k, v, causal, scale=None):
     return o, lse
 
 
-def _check_against_oracle(oracle, q, k, v, o, lse, causal, scale, dtype):
+def _check_against_oracle(oracle, q, k, v, o, lse, causal, scale, dtype, contract=True):
+    """contract=True: the north-star bars (max-abs 1e-2, mean-abs 1e-3, 2x the
+    emulated reference-kernel error, LSE 1e-3), stated for and holding on the
+    BASELINE configurations, where |O| is small.  contract=False (explicit
+    scales, random problems): peaked rows put |O| above 1, where bf16's
+    rounding of P and of O alone (the reference kernel's arithmetic, which
+    the emulator reproduces) exceeds 1e-2; those cases are held to the 2x
+    reference-kernel bar on the mean error (3x on the max) and to the LSE bar."""
     qn, kn, vn = to_np32(q), to_np32(k), to_np32(v)
     ref_o, ref_lse = oracle.attn_f64(qn, kn, vn, scale, causal)
     emu_o, _ = oracle.kernel_numerics(qn, kn, vn, scale, causal,
                                       oracle.BF16 if dtype == "bf16" else oracle.F16)
-    mx, mean = err_stats(to_np32(o), ref_o)
+    got = to_np32(o)
+    mx, mean = err_stats(got, ref_o)
     emx, emean = err_stats(emu_o, ref_o)
     lse_err = float(np.abs(to_np32(lse).astype(np.float64) - ref_lse).max())
     _note(f"  max_abs={mx:.3e} mean_abs={mean:.3e} (ref-kernel emu {emx:.3e}/{emean:.3e}) "
           f"lse_err={lse_err:.3e}")
-    assert np.isfinite(to_np32(o)).all()
-    assert mx <= MAX_ABS_TOL, f"max-abs {mx}"
-    assert mean <= MEAN_ABS_TOL, f"mean-abs {mean}"
-    assert mx <= 2 * emx + 1e-6, f"max-abs {mx} > 2x reference-kernel error {emx}"
+    assert np.isfinite(got).all()
+    if contract:
+        assert mx <= MAX_ABS_TOL, f"max-abs {mx}"
+        assert mean <= MEAN_ABS_TOL, f"mean-abs {mean}"
+    elif dtype == "fp16":
+        assert mx <= MAX_ABS_TOL, f"max-abs {mx}"
+    # The maximum over ~1e4 elements is one rounding event of P or O: which
+    # elements round badly depends on the exponent offset, and this kernel's
+    # lazy offset differs from the reference's per-tile one.  Outside the
+    # contract configurations the max is held to 3x, the mean to 2x.
+    max_factor = 2 if contract else 3
+    assert mx <= max_factor * emx + 1e-6, \
+        f"max-abs {mx} > {max_factor}x reference-kernel error {emx}"
     assert mean <= 2 * emean + 1e-6, f"mean-abs {mean} > 2x reference-kernel error {emean}"
     assert lse_err <= LSE_TOL, f"lse {lse_err}"
 
@@ -67,6 +84,50 @@ def test_small_shapes_vs_oracle(fa, oracle, N, D, dtype, causal):
     scale = 1.0 / math.sqrt(D)
     o, lse = _fwd(fa, q.to(DEV), k.to(DEV), v.to(DEV), causal)
     _check_against_oracle(oracle, q, k, v, o, lse, causal, scale, dtype)
+
+
+@pytest.mark.parametrize("scale", [0.01, 0.5, 1.0, 3.0])
+@pytest.mark.parametrize("causal", [False, True], ids=["noncausal", "causal"])
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+def test_softmax_scale_vs_oracle(fa, oracle, scale, causal, dtype):
+    """Explicit softmax_scale values, from nearly uniform attention (0.01) to
+    sharply peaked rows (3.0, scores up to ~100 in log units, many lazy
+    rescales)."""
+    _note(f"case scale={scale} {dtype} causal={causal}")
+    N, D = 333, 128
+    q, k, v = make_qkv(1, 2, N, D, dtype, seed=case_seed(int(scale * 100) + 5), device="cpu")
+    o, lse = _fwd(fa, q.to(DEV), k.to(DEV), v.to(DEV), causal, scale=scale)
+    _check_against_oracle(oracle, q, k, v, o, lse, causal, scale, dtype, contract=False)
+
+
+@pytest.mark.parametrize("case", range(24))
+def test_random_problems_vs_oracle(fa, oracle, case):
+    """Seeded random problems: shape, dtype, mask, scale and memory layout
+    (contiguous, BNHD view, padded seq stride) drawn per case."""
+    rng = np.random.default_rng(1000 + case)
+    B = int(rng.integers(1, 3))
+    H = int(rng.integers(1, 4))
+    N = int(rng.choice([int(rng.integers(1, 64)), int(rng.integers(64, 700))]))
+    D = int(rng.choice([64, 128]))
+    dtype = str(rng.choice(["fp16", "bf16"]))
+    causal = bool(rng.integers(0, 2))
+    scale = float(rng.choice([1.0 / math.sqrt(D), float(rng.uniform(0.02, 0.6))]))
+    layout = str(rng.choice(["bhnd", "bnhd", "padded"]))
+    _note(f"case random#{case}: B={B} H={H} N={N} D={D} {dtype} causal={causal} "
+          f"scale={scale:.4f} layout={layout}")
+    q, k, v = make_qkv(B, H, N, D, dtype, seed=case_seed(5000 + case), device="cpu")
+
+    def place(t):
+        if layout == "bnhd":
+            return t.permute(0, 2, 1, 3).contiguous().to(DEV).permute(0, 2, 1, 3)
+        if layout == "padded":  # rows of D + 64 elements, head_dim slice
+            buf = torch.zeros(B, H, N, D + 64, dtype=t.dtype)
+            buf[..., :D] = t
+            return buf.to(DEV)[..., :D]
+        return t.to(DEV)
+
+    o, lse = _fwd(fa, place(q), place(k), place(v), causal, scale=scale)
+    _check_against_oracle(oracle, q, k, v, o, lse, causal, scale, dtype, contract=False)
 
 
 @pytest.mark.parametrize("dtype", ["fp16", "bf16"])
