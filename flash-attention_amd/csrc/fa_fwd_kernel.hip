@@ -5,7 +5,10 @@
 // (src/loadstore, src/tensor_core, src/softmax, src/ptx).  It is written for
 // the CDNA4 execution model rather than translated from the mma.sync design:
 //
-//  * One workgroup = NW wave64s, each wave owns 32 query rows (BM = 32*NW).
+//  * One workgroup = NW wave64s, each wave owns 32 query rows (BM = 32*NW):
+//    NW = 4 with two workgroups per CU, or NW = 8 (one workgroup per CU,
+//    half the staging traffic per flop) for long non-causal rows; either
+//    way two waves share each SIMD.
 //  * S^T = K * Q^T on v_mfma_f32_32x32x16_{f16,bf16}: K tile rows are the A
 //    operand (read from LDS), Q rows are the B operand (kept in VGPRs for the
 //    whole kernel).  In the 32x32 accumulator layout lane l holds column
@@ -24,9 +27,8 @@
 //    (ds_read_b128) and the V transposed reads hit distinct banks.
 //  * LDS operands are read a few MFMAs ahead of use (K: 3 k-steps, V: 4
 //    MFMAs, the first V reads overlapping the softmax) so each MFMA finds its
-//    operand ready; two workgroups share a CU (2 waves per SIMD), and the
-//    wave issuing PV MFMAs runs at raised priority so the other wave's
-//    softmax fills the VALU in the meantime.
+//    operand ready, and the wave issuing PV MFMAs runs at raised priority so
+//    the other wave on its SIMD fills the VALU with its softmax meanwhile.
 //  * Causal: fully-masked K tiles are never loaded or computed; q-tiles are
 //    dispatched longest-first.  Ragged N: loads clamp to the last row and the
 //    scores of keys >= N are -inf; rows >= N are never stored.
@@ -34,12 +36,15 @@
 //    q-tiles of the same heads.
 //
 // Numerics follow the reference (src/softmax/online_softmax.cuh:13-19,
-// :89-152; src/forward/forward_v6_mma.cuh:19-38): fp32 scores, running max m
-// of the raw scores, p = exp2(s*c - m*c) with c = scale*log2(e), O and l
-// rescaled by exp2((m_old - m_new)*c), P rounded to the input type with
-// round-to-nearest-even before the PV product, l summed from the unrounded
-// fp32 p, O normalised in fp32 and rounded to the input type.  New relative to
-// the reference: the natural-log LSE = m*scale + ln(l).
+// :89-152; src/forward/forward_v6_mma.cuh:19-38): fp32 scores, an exponent
+// offset m taken from the raw scores, p = exp2(s*c - m*c) with
+// c = scale*log2(e), O and l rescaled by exp2((m_old - m_new)*c), P rounded
+// to the input type with round-to-nearest-even before the PV product, O
+// normalised in fp32 and rounded to the input type.  Differences: m is raised
+// only when a row's max exceeds it by more than kRescaleThreshold (the
+// common factor cancels in O/l); fp16 sums the rounded P into l (the weights
+// P V actually uses), bf16 the unrounded p as the reference; and the
+// natural-log LSE = m*scale + ln(l) is new.
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
