@@ -201,6 +201,34 @@ def cpu_baseline(name, budget_s=15.0):
     }
 
 
+def cpu_torch_baseline(name, budget_s=5.0):
+    """torch's CPU scaled_dot_product_attention in fp32 on whole heads of the
+    workload (the reference harness's pytorch baseline, benchmark_pybind.py:
+    129-132, run on the host), all torch threads; returns TFLOP/s."""
+    import torch
+
+    B, H, N, D, dtype, causal, sigma, case = WORKLOADS[name]
+    (q, k, v), _ = make_inputs(torch, name, "cpu")
+    qf, kf, vf = (t.reshape(B * H, 1, N, D).float() for t in (q, k, v))
+    sdpa = torch.nn.functional.scaled_dot_product_attention
+    per_head = flops(1, 1, N, D, causal)
+    t0 = time.perf_counter()
+    sdpa(qf[:1], kf[:1], vf[:1], is_causal=causal)
+    dt1 = max(time.perf_counter() - t0, 1e-4)
+    heads = int(max(1, min(B * H, budget_s / dt1)))
+    t0 = time.perf_counter()
+    for i in range(heads):
+        sdpa(qf[i:i + 1], kf[i:i + 1], vf[i:i + 1], is_causal=causal)
+    dt = time.perf_counter() - t0
+    return {
+        "value": per_head * heads / dt / 1e12,
+        "unit": "TFLOPS",
+        "cores": torch.get_num_threads(),
+        "kind": "torch-cpu",
+        "sample": f"{heads} of {B * H} heads of {name}, fp32 SDPA, {dt:.1f} s",
+    }
+
+
 def main():
     ap = argparse.ArgumentParser(description="MI355X FlashAttention-2 forward benchmark")
     ap.add_argument("--gpus", type=int, default=1)
@@ -276,6 +304,7 @@ def main():
 
     cold_ms, cold_tflops = time_cold(torch, fa, name, 20, args.input_mode)
     cpu = None if args.no_cpu_baseline else cpu_baseline(name)
+    cpu_torch = None if args.no_cpu_baseline else cpu_torch_baseline(name)
 
     line = {
         "metric": "fwd TFLOPS + % of FP16 MFMA peak, B4 H32 N4096 D128 fp16 (1 GPU)",
@@ -307,6 +336,7 @@ def main():
             "traffic": traffic,
         },
         "cpu_baseline": cpu,
+        "cpu_baseline_torch": cpu_torch,
         "cold": {"ms_per_step": round(cold_ms, 5), "tflops": round(cold_tflops, 2),
                  "note": "median of 20 launches, each after a 512 MiB cache flush"},
         "device": {k: info[k] for k in ("arch", "compute_units", "clock_khz",
