@@ -65,7 +65,6 @@ struct Tile {
   static constexpr int BN = 64;                 // keys per K/V tile
   static constexpr int ROWB = D * 2;            // bytes per K/V row
   static constexpr int BYTES = BN * ROWB;       // bytes per K or V tile
-  static constexpr int CHUNKS = ROWB / 16;      // 16-byte chunks per row
   // K tile: the 32x32x16 A-operand read is ds_read_b128 of one 16-byte chunk
   // per lane for 32 consecutive keys; XOR the chunk index with key bits so
   // consecutive keys land on distinct bank groups.
