@@ -198,8 +198,9 @@ fa_status fa_device_info(int device, fa_device_info_t* out) {
   const hipError_t e = hipGetDeviceProperties(&prop, device);
   if (e != hipSuccess)
     return fail(FA_ERR_HIP, "hipGetDeviceProperties(%d) failed: %s", device, hipGetErrorString(e));
-  std::snprintf(out->name, sizeof(out->name), "%s", prop.name);
   std::snprintf(out->arch, sizeof(out->arch), "%s", prop.gcnArchName);
+  // Some driver installs report an empty marketing name; fall back to the ISA.
+  std::snprintf(out->name, sizeof(out->name), "%s", prop.name[0] ? prop.name : prop.gcnArchName);
   out->compute_units = prop.multiProcessorCount;
   out->clock_khz = prop.clockRate;
   out->lds_per_cu_bytes = (int64_t)prop.maxSharedMemoryPerMultiProcessor;
@@ -208,7 +209,13 @@ fa_status fa_device_info(int device, fa_device_info_t* out) {
   out->memory_clock_khz = prop.memoryClockRate;
   // CDNA4: 2048 dense fp16/bf16 FMA = 4096 flop per clock per CU.
   out->fp16_dense_peak_tflops = (double)prop.multiProcessorCount * prop.clockRate * 1e3 * 4096.0 / 1e12;
-  out->hbm_peak_gbps = 2.0 * prop.memoryClockRate * 1e3 * (prop.memoryBusWidth / 8.0) / 1e9;
+  // The DDR formula below does not hold for HBM3E's data rate; for gfx950
+  // (MI355X) use the published 8 TB/s, as the reference keys its peak table
+  // on the device (perf_metrics.cuh:78-120).
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) == 0)
+    out->hbm_peak_gbps = 8000.0;
+  else
+    out->hbm_peak_gbps = 2.0 * prop.memoryClockRate * 1e3 * (prop.memoryBusWidth / 8.0) / 1e9;
   return FA_OK;
 }
 

@@ -91,7 +91,8 @@ typedef struct {
   int32_t memory_clock_khz;
   /* compute_units x clock x 4096 dense fp16/bf16 MFMA flop per clock per CU */
   double fp16_dense_peak_tflops;
-  /* 2 x bus width x memory clock (DDR) */
+  /* published 8000 GB/s for gfx950 (MI355X); 2 x bus width x memory clock
+   * (DDR) for other devices */
   double hbm_peak_gbps;
 } fa_device_info_t;
 
