@@ -47,3 +47,19 @@ def test_fa_profile_csv_line(extra):
     assert len(f) == 13
     assert f[1:5] == ["2", "2", "300", "64"]
     assert float(f[5]) > 0 and float(f[6]) > 0
+
+
+def test_device_info_mi355x(fa):
+    """The device query behind %-of-peak figures (replaces
+    utils/get_gpu_hardware_param.cu): gfx950 with 256 CUs, the dense fp16
+    MFMA peak derived from CUs x clock x 4096, and the published HBM rate."""
+    print("case device_info", flush=True)
+    info = fa.device_info(0)
+    assert info["arch"].startswith("gfx950")
+    assert info["name"]
+    assert info["compute_units"] == 256
+    expect = info["compute_units"] * info["clock_khz"] * 1e3 * 4096 / 1e12
+    assert abs(info["fp16_dense_peak_tflops"] - expect) < 1e-6 * expect
+    assert 2000 < info["fp16_dense_peak_tflops"] < 3000
+    assert info["hbm_peak_gbps"] == 8000.0
+    assert info["lds_per_cu_bytes"] >= 64 * 1024
