@@ -350,3 +350,32 @@ def test_runtime_product_path_has_no_cpu_fallback():
             "    print('IMPORTED')\n")
     out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120)
     assert "IMPORT-FAILED" in out.stdout, out.stdout + out.stderr
+
+
+def test_last_error_is_thread_local(lib):
+    """Each thread sees the detail of its own last failure (the only mutable
+    global state of the library is this thread-local string)."""
+    import threading
+
+    results = {}
+
+    def worker(idx):
+        p = contiguous(dtype=idx + 10) if idx % 2 else contiguous(D=128)
+        if idx % 2 == 0:
+            p.head_dim = 96
+        for _ in range(200):
+            rc = lib.fa_fwd_validate(ctypes.byref(p))
+            msg = lib.fa_last_error().decode()
+            ok = (rc == A.FA_ERR_DTYPE and f"dtype {idx + 10}" in msg) if idx % 2 else \
+                 (rc == A.FA_ERR_HEADDIM and "got 96" in msg)
+            if not ok:
+                results[idx] = (rc, msg)
+                return
+        results[idx] = "ok"
+
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(8)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert all(v == "ok" for v in results.values()), results

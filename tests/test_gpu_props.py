@@ -97,3 +97,22 @@ def test_hip_graph_replay_matches_eager(fa, name):
         e = fa.forward(q, k, v, causal=causal)
         torch.cuda.synchronize()
         assert torch.equal(e, ref)
+
+
+def test_concurrent_streams_match_sequential(fa):
+    """fa_fwd is re-entrant and asynchronous on the caller's stream: four
+    problems launched on four streams at once give the sequential results."""
+    _note("case concurrent streams")
+    probs = [make_config(n, device=DEV) for n in ("C2", "C5r")] * 2
+    ref = [fa.forward(q, k, v, causal=c) for q, k, v, c, _ in probs]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream() for _ in probs]
+    outs = [torch.empty_like(p[0]) for p in probs]
+    for st in streams:
+        st.wait_stream(torch.cuda.current_stream())
+    for (q, k, v, c, _), st, o in zip(probs, streams, outs):
+        with torch.cuda.stream(st):
+            fa.forward(q, k, v, o, causal=c)
+    torch.cuda.synchronize()
+    for o, r in zip(outs, ref):
+        assert torch.equal(o, r)
