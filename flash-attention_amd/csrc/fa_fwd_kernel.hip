@@ -40,11 +40,12 @@
 // offset m taken from the raw scores, p = exp2(s*c - m*c) with
 // c = scale*log2(e), O and l rescaled by exp2((m_old - m_new)*c), P rounded
 // to the input type with round-to-nearest-even before the PV product, O
-// normalised in fp32 and rounded to the input type.  Differences: m is raised
-// only when a row's max exceeds it by more than kRescaleThreshold (the
-// common factor cancels in O/l); fp16 sums the rounded P into l (the weights
-// P V actually uses), bf16 the unrounded p as the reference; and the
-// natural-log LSE = m*scale + ln(l) is new.
+// normalised in fp32 and rounded to the input type.  Differences: m is an
+// offset at or below the running max, raised only when a tile's P would
+// reach 2^15 (the common factor exp2(m_max*c - m*c) cancels in O/l), so the
+// row max is computed only on such tiles; fp16 sums the rounded P into l
+// (the weights P V actually uses), bf16 the unrounded p as the reference;
+// and the natural-log LSE = m*scale + ln(l) is new.
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -92,10 +93,13 @@ __device__ __forceinline__ void dma_slot(int wave, int it, int lane, int& r, int
   c = pc ^ (IS_V ? T::swz_v(r) : T::swz_k(r));
 }
 
-// Exponent offset threshold (log2 units) for the lazy rescale: the max used
-// in p = exp2(s*c - m*c) is only raised when a row's new max exceeds it by
-// more than this, so p <= 2^8 between rescales (safe in fp16/bf16 P and in
-// the fp32 O and l accumulators) and O/l are rescaled only on such raises.
+// Lazy exponent offset.  The offset m in p = exp2(s*c - m*c) is re-derived
+// from the row max only when a tile's P sum (per lane, 32 keys) reaches
+// kSumLimit; every P then stays below 2^15, finite in fp16 (max 65504) and
+// far from overflow in the fp32 O and l accumulators.  When it is re-derived,
+// m moves to the row max for rows that exceed it by more than
+// kRescaleThreshold (log2 units).
+constexpr float kSumLimit = 32768.0f;
 constexpr float kRescaleThreshold = 8.0f;
 
 // Operand prefetch depths (measured best on MI355X): K operands for S^T are
@@ -213,9 +217,9 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
 #pragma unroll
     for (int i = 0; i < 16; ++i) o_acc[db][i] = 0.0f;
   const float c = args.scale_log2;
-  float m_run = -INFINITY;  // max used in the exponent (<= true running max + threshold)
-  float neg_mc = 0.0f;      // -m_run * c (0 while m_run = -inf)
-  float l_run0 = 0.0f, l_run1 = 0.0f;  // this lane's partial sums of P
+  float m_run = -INFINITY;  // offset used in the exponent (<= the running max)
+  float neg_mc = INFINITY;  // -m_run * c; +inf while m_run = -inf (trips the first check)
+  float l_run = 0.0f;       // this lane's partial sum of P
 
   // Per-lane LDS byte offsets inside a tile (loop invariant).
   // K: A operand of key block kb, k-step kk -> row kb*32 + l32, chunk 2kk+g.
@@ -302,54 +306,74 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
         }
     }
 
-    // ---- online softmax with lazy rescale (reference online_softmax.cuh:89-152) ----
-    const float mx = pair_max(max32(s[0], s[1]));
-    const bool grow = (mx - m_run) * c > kRescaleThreshold;  // false for NaN (-inf - -inf)
-    if (__any(grow)) {
+    // ---- P = exp2(s*c - m*c) with the current offset m, and its tile sums ----
+    // P is packed as the P^T B operand: chunk ch = 2kb + hh uses S registers
+    // 8hh..8hh+7 of block kb.  t0/t1 sum this lane's even/odd keys.
+    i16x8 pf[4];
+    float t0, t1;
+    auto exp_pack = [&](float nmc) FA_INLINE {
+      t0 = 0.0f;
+      t1 = 0.0f;
+#pragma unroll
+      for (int ch = 0; ch < 4; ++ch) {
+        const int kb = ch >> 1, base = (ch & 1) * 8;
+        u32x4 w;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float p0 = fast_exp2(fmaf(s[kb][base + 2 * j], c, nmc));
+          const float p1 = fast_exp2(fmaf(s[kb][base + 2 * j + 1], c, nmc));
+          w[j] = pack2<BF16>(p0, p1);
+          if constexpr (BF16) {
+            // bf16 keeps 8 significant bits: sum the unrounded fp32 p (as
+            // the reference does, online_softmax.cuh:135-152) so the LSE
+            // stays accurate to ~1e-6 instead of ~2^-8.
+            t0 += p0;
+            t1 += p1;
+          }
+        }
+        pf[ch] = __builtin_bit_cast(i16x8, w);
+        if constexpr (!BF16) {
+          // fp16: sum the rounded P (the values that enter P V; relative
+          // error <= 2^-11 per term) with v_dot2c_f32_f16, 2 terms per op.
+          t0 = dot2_acc<BF16>(w[0], t0);
+          t1 = dot2_acc<BF16>(w[1], t1);
+          t0 = dot2_acc<BF16>(w[2], t0);
+          t1 = dot2_acc<BF16>(w[3], t1);
+        }
+      }
+    };
+    exp_pack(neg_mc);
+
+    // ---- online softmax with a lazy offset (reference online_softmax.cuh:89-152) ----
+    // m need not be the running max: any m <= it gives the same O and l up
+    // to a common factor that cancels in O / l.  It only has to keep every P
+    // finite and below kSumLimit.  The tile sums check exactly that (a sum
+    // bounds each of its terms, and is inf or NaN if a P overflowed or
+    // m = -inf), so the row max is taken only when a sum reaches the limit:
+    // on the first tile of a row, or when the scores jump by more than
+    // ~15/c.  Then m moves to the row max for rows whose max exceeds it by
+    // more than kRescaleThreshold (each row that tripped the check does), O
+    // and l are rescaled, and P is recomputed.
+    if (__any(!(t0 + t1 < kSumLimit))) {
+      const float mx = pair_max(max32(s[0], s[1]));
+      const bool grow = (mx - m_run) * c > kRescaleThreshold;  // false for NaN (-inf - -inf)
       const float m_new = grow ? mx : m_run;
-      // exp2(0) = 1 for rows that keep their max (branch-free: also covers
-      // m_run = -inf, where m_run - m_new would be NaN).
+      // exp2(0) = 1 for rows that keep their offset (branch-free: also
+      // covers m_run = -inf, where m_run - m_new would be NaN).
       const float alpha = fast_exp2(grow ? (m_run - m_new) * c : 0.0f);
       m_run = m_new;
-      neg_mc = -(m_run == -INFINITY ? 0.0f : m_run) * c;
-      l_run0 *= alpha;
-      l_run1 *= alpha;
+      l_run *= alpha;
 #pragma unroll
       for (int db = 0; db < DBLK; ++db)
 #pragma unroll
         for (int i = 0; i < 16; ++i) o_acc[db][i] *= alpha;
+      // A row whose keys were all masked keeps m = -inf: its P is 0 now
+      // (offset 0) and its next tile trips the check again (offset +inf).
+      const bool none = m_run == -INFINITY;
+      neg_mc = none ? INFINITY : -m_run * c;
+      exp_pack(none ? 0.0f : neg_mc);
     }
-
-    // ---- P = exp2(s*c - m*c), packed as the P^T B operand ----
-    // chunk ch = 2kb + hh uses S registers 8hh..8hh+7 of block kb.
-    i16x8 pf[4];
-#pragma unroll
-    for (int ch = 0; ch < 4; ++ch) {
-      const int kb = ch >> 1, base = (ch & 1) * 8;
-      u32x4 w;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float p0 = fast_exp2(fmaf(s[kb][base + 2 * j], c, neg_mc));
-        const float p1 = fast_exp2(fmaf(s[kb][base + 2 * j + 1], c, neg_mc));
-        w[j] = pack2<BF16>(p0, p1);
-        if constexpr (BF16) {
-          // bf16 keeps 8 significant bits: sum the unrounded fp32 p (as the
-          // reference does, online_softmax.cuh:135-152) so the LSE stays
-          // accurate to ~1e-6 instead of ~2^-8.
-          l_run0 += p0;
-          l_run1 += p1;
-        }
-      }
-      pf[ch] = __builtin_bit_cast(i16x8, w);
-      if constexpr (!BF16) {
-        // fp16: sum the rounded P (the values that enter P V; relative
-        // error <= 2^-11 per term) with v_dot2c_f32_f16, 2 terms per op.
-        l_run0 = dot2_acc<BF16>(w[0], l_run0);
-        l_run1 = dot2_acc<BF16>(w[1], l_run1);
-        l_run0 = dot2_acc<BF16>(w[2], l_run0);
-        l_run1 = dot2_acc<BF16>(w[3], l_run1);
-      }
-    }
+    l_run += t0 + t1;
 
     // ---- O^T += V^T P^T ----
     // Raised wave priority while this wave issues its PV MFMAs: the other
@@ -386,8 +410,7 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
   }
 
   // ---- epilogue: combine the two half-row partial sums, normalise, store ----
-  const float l_lane = l_run0 + l_run1;
-  const float l_tot = pair_sum(l_lane);
+  const float l_tot = pair_sum(l_run);
   const bool row_ok = qrow < N;
   const float inv_l = (row_ok && l_tot > 0.0f) ? 1.0f / l_tot : 0.0f;
   if (row_ok) {

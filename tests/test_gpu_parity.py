@@ -100,6 +100,46 @@ def test_softmax_scale_vs_oracle(fa, oracle, scale, causal, dtype):
     _check_against_oracle(oracle, q, k, v, o, lse, causal, scale, dtype, contract=False)
 
 
+def _scale_keys(k, pattern):
+    """K with some key rows multiplied so that scores jump inside a row:
+    jump  - tile 3 (keys 192..255) x8: the offset is re-derived mid-row;
+    ramp  - key j x (1 + 6j/N): the max rises on every tile;
+    half  - keys j = 4..7 mod 8 of tile 2 x8: only one lane half of each row
+            (keys 8a + 4g + b, g = lane half) sees the jump;
+    drop  - tile 0 x8: the first tile holds the max, later P are tiny."""
+    k = k.float()
+    N = k.shape[2]
+    f = torch.ones(N)
+    j = torch.arange(N)
+    if pattern == "jump":
+        f[192:256] = 8.0
+    elif pattern == "ramp":
+        f = 1.0 + 6.0 * j / N
+    elif pattern == "half":
+        f[(j >= 128) & (j < 192) & (j % 8 >= 4)] = 8.0
+    elif pattern == "drop":
+        f[:64] = 8.0
+    return k * f[None, None, :, None]
+
+
+@pytest.mark.parametrize("pattern", ["jump", "ramp", "half", "drop"])
+@pytest.mark.parametrize("causal", [False, True], ids=["noncausal", "causal"])
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+def test_score_jumps_vs_oracle(fa, oracle, pattern, causal, dtype):
+    """Rows whose scores jump between key tiles: the kernel's exponent offset
+    is re-derived only when a tile's P sum would reach 2^15, which these
+    inputs force mid-row, on every tile, in one lane half only, or never
+    after the first tile."""
+    _note(f"case jumps pattern={pattern} {dtype} causal={causal}")
+    N, D = 640, 128
+    q, k, v = make_qkv(1, 2, N, D, dtype, seed=case_seed(777), device="cpu")
+    tdt = torch.float16 if dtype == "fp16" else torch.bfloat16
+    k = _scale_keys(k, pattern).to(tdt)
+    scale = 1.0 / math.sqrt(D)
+    o, lse = _fwd(fa, q.to(DEV), k.to(DEV), v.to(DEV), causal)
+    _check_against_oracle(oracle, q, k, v, o, lse, causal, scale, dtype, contract=False)
+
+
 @pytest.mark.parametrize("case", range(24))
 def test_random_problems_vs_oracle(fa, oracle, case):
     """Seeded random problems: shape, dtype, mask, scale and memory layout
