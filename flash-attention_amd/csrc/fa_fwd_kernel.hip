@@ -43,9 +43,10 @@
 // normalised in fp32 and rounded to the input type.  Differences: m is an
 // offset at or below the running max, raised only when a tile's P would
 // reach 2^15 (the common factor exp2(m_max*c - m*c) cancels in O/l), so the
-// row max is computed only on such tiles; fp16 sums the rounded P into l
-// (the weights P V actually uses), bf16 the unrounded p as the reference;
-// and the natural-log LSE = m*scale + ln(l) is new.
+// row max is computed only on such tiles; fp16 at D = 128 sums the rounded P
+// into l (the weights P V actually uses), bf16 and fp16 at D = 64 the
+// unrounded p as the reference; and the natural-log LSE = m*scale + ln(l)
+// is new.
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -120,6 +121,11 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
   constexpr int KSTEPS = D / 16;  // MFMA k-steps for S^T (k = head dim)
   constexpr int DBLK = D / 32;    // 32-wide head-dim blocks of O^T
   constexpr int ITERS = T::BYTES / (1024 * NW);  // DMA instructions per wave per tile
+  // Row sums of P: fp32 sums of the unrounded p for bf16, and for fp16 at
+  // D = 64, where the softmax is twice as dense per MFMA and two v_add_f32
+  // issue faster than one v_dot2c_f32_f16 (+8 % at B4 H16 N1024 D64);
+  // fp16 at D = 128 sums the rounded P with v_dot2c (same speed there).
+  constexpr bool kUnroundedSum = BF16 || D == 64;
   static_assert(ITERS >= 1 && T::BYTES % (1024 * NW) == 0, "tile must split evenly over waves");
 
   // LDS ring: K buffers 0/1 then V buffers 0/1.
@@ -323,18 +329,18 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
           const float p0 = fast_exp2(fmaf(s[kb][base + 2 * j], c, nmc));
           const float p1 = fast_exp2(fmaf(s[kb][base + 2 * j + 1], c, nmc));
           w[j] = pack2<BF16>(p0, p1);
-          if constexpr (BF16) {
-            // bf16 keeps 8 significant bits: sum the unrounded fp32 p (as
-            // the reference does, online_softmax.cuh:135-152) so the LSE
-            // stays accurate to ~1e-6 instead of ~2^-8.
+          if constexpr (kUnroundedSum) {
+            // Sum the unrounded fp32 p, as the reference does
+            // (online_softmax.cuh:135-152).  bf16 needs it: its 8
+            // significant bits would cost up to 2^-9 in the LSE.
             t0 += p0;
             t1 += p1;
           }
         }
         pf[ch] = __builtin_bit_cast(i16x8, w);
-        if constexpr (!BF16) {
-          // fp16: sum the rounded P (the values that enter P V; relative
-          // error <= 2^-11 per term) with v_dot2c_f32_f16, 2 terms per op.
+        if constexpr (!kUnroundedSum) {
+          // fp16, D = 128: sum the rounded P (the values that enter P V;
+          // relative error <= 2^-11 per term) with v_dot2c_f32_f16.
           t0 = dot2_acc<BF16>(w[0], t0);
           t1 = dot2_acc<BF16>(w[1], t1);
           t0 = dot2_acc<BF16>(w[2], t0);
