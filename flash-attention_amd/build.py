@@ -4,6 +4,7 @@ Outputs (next to the Python package, so they travel with the repository):
   flash_attention_runtime/libfa_mi355x.so   HIP kernels + C ABI (hipcc, gfx950)
   flash_attention_runtime/_C<EXT_SUFFIX>     torch/pybind binding over the C ABI
   flash_attention_runtime/fa_profile         C++ benchmark CLI over the C ABI
+  flash_attention_runtime/fa_mfma_probe      MFMA-only throughput probe (peak cross-check)
 
 Replaces the reference's JIT build (python/flash_attention_runtime/
 __init__.py:10-27, torch.utils.cpp_extension.load of _ext.cu with nvcc) by an
@@ -124,11 +125,22 @@ def build_profile_cli() -> str:
     return out
 
 
+def build_mfma_probe() -> str:
+    """Builds the fa_mfma_probe executable (csrc/fa_mfma_probe.hip), which
+    times MFMA-only waves to cross-check the computed MFMA peak."""
+    out = os.path.join(OUT_DIR, "fa_mfma_probe")
+    _run([_hipcc(), *[f for f in HIP_FLAGS if f != "-fPIC"],
+          os.path.join(CSRC, "fa_mfma_probe.hip"), "-o", out + ".tmp"])
+    os.replace(out + ".tmp", out)
+    return out
+
+
 def build(jobs: int = 8) -> list[str]:
     lib = build_hip_library(jobs)
     ext = build_torch_binding()
     cli = build_profile_cli()
-    return [lib, ext, cli]
+    probe = build_mfma_probe()
+    return [lib, ext, cli, probe]
 
 
 def main() -> None:
