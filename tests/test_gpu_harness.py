@@ -63,3 +63,25 @@ def test_device_info_mi355x(fa):
     assert 2000 < info["fp16_dense_peak_tflops"] < 3000
     assert info["hbm_peak_gbps"] == 8000.0
     assert info["lds_per_cu_bytes"] >= 64 * 1024
+
+
+PROBE = os.path.join(REPO, "flash-attention_amd", "flash_attention_runtime", "fa_mfma_probe")
+
+
+def test_mfma_probe_reaches_formula_peak():
+    """The MFMA-only probe: with low-toggle operands and one wave per SIMD the
+    matrix cores must run near the CUs x clock x 4096 figure the benchmark
+    divides by (a short run, before the power limiter settles)."""
+    print("case fa_mfma_probe", flush=True)
+    r = subprocess.run([PROBE, "--ms", "2", "--rounds", "1"], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 0, r.stderr
+    rows = {}
+    for ln in r.stdout.splitlines():
+        f = ln.split()
+        if len(f) >= 4 and f[0] in ("ones", "N(0,1)") and f[1] in ("1", "2"):
+            rows[(f[0], int(f[1]))] = (float(f[2]), float(f[3].rstrip("%")))
+    assert set(rows) == {("ones", 1), ("ones", 2), ("N(0,1)", 1), ("N(0,1)", 2)}
+    assert rows[("ones", 1)][1] > 85.0, rows
+    for tflops, pct in rows.values():
+        assert 0.0 < pct <= 101.0 and tflops > 0.0
