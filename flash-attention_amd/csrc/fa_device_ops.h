@@ -27,6 +27,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef short i16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
@@ -82,6 +83,28 @@ __device__ __forceinline__ float dot2_acc(uint32_t w, float acc) {
     const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
     return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w), one, acc, false);
   }
+}
+
+// Row sums of P on the matrix core.  A P^T chunk register (the B operand of
+// the 32x32x16 PV product: lane l holds 8 keys of query row l % 32, key half
+// l / 32) read as the B operand of v_mfma_f32_16x16x32_f16 has
+// B[k = 8*(l/16) + j][n = l % 16]: k-groups 0 and 2 are rows 0..15, groups
+// 1 and 3 rows 16..31.  With the selector A (row 0 = ones on k-groups 0 and 2,
+// row 1 = ones on groups 1 and 3, other rows 0) the product adds the chunk's
+// 16-key sum of row n to C[0][n] and of row n + 16 to C[1][n]; lane n < 16
+// holds C[0][n] in element 0 and C[1][n] in element 1.
+__device__ __forceinline__ f16x8 row_sum_selector(int lane) {
+  const _Float16 one = ((lane & 15) == ((lane >> 4) & 1)) ? (_Float16)1.0f : (_Float16)0.0f;
+  return f16x8{one, one, one, one, one, one, one, one};
+}
+__device__ __forceinline__ f32x4 row_sum_mfma(f16x8 sel, i16x8 p, f32x4 acc) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(sel, __builtin_bit_cast(f16x8, p), acc, 0, 0, 0);
+}
+// The accumulated sum of lane `lane`'s query row (row lane % 32).
+__device__ __forceinline__ float row_sum_of_lane(f32x4 acc, int lane) {
+  const float lo = __shfl(acc[0], lane & 15);
+  const float hi = __shfl(acc[1], lane & 15);
+  return (lane & 31) < 16 ? lo : hi;
 }
 
 // Compile-time loop: f(std::integral_constant<int, I>) for I in [B, E).

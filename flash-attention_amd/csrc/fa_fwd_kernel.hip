@@ -43,9 +43,11 @@
 // normalised in fp32 and rounded to the input type.  Differences: m is an
 // offset at or below the running max, raised only when a tile's P would
 // reach 2^15 (the common factor exp2(m_max*c - m*c) cancels in O/l), so the
-// row max is computed only on such tiles; fp16 at D = 128 sums the rounded P
-// into l (the weights P V actually uses), bf16 and fp16 at D = 64 the
-// unrounded p as the reference; and the natural-log LSE = m*scale + ln(l)
+// row max is computed only on such tiles (non-causal fp16 at D = 128 runs an
+// optimistic pass with the offset of the first tile and redoes the workgroup
+// with per-tile checks only if a P overflowed); fp16 at D = 128 sums the
+// rounded P into l (the weights P V actually uses), bf16 and fp16 at D = 64
+// the unrounded p as the reference; and the natural-log LSE = m*scale + ln(l)
 // is new.
 
 #include <hip/hip_runtime.h>
@@ -124,12 +126,27 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
   // Row sums of P: fp32 sums of the unrounded p for bf16, and for fp16 at
   // D = 64, where the softmax is twice as dense per MFMA and two v_add_f32
   // issue faster than one v_dot2c_f32_f16 (+8 % at B4 H16 N1024 D64);
-  // fp16 at D = 128 sums the rounded P with v_dot2c (same speed there).
+  // fp16 at D = 128 sums the rounded P (v_dot2c, or the matrix core below).
   constexpr bool kUnroundedSum = BF16 || D == 64;
+  // fp16, D = 128, non-causal: the rounded-P row sums run on the matrix core
+  // (row_sum_mfma, 4 small MFMAs per tile in place of 16 v_dot2c; +3 % at
+  // B4 H32 N4096, neutral for the causal kernels, which keep v_dot2c), and the
+  // kernel runs an optimistic pass first: the offset m is taken from the row
+  // max of the first key tile only and never checked again.  The check
+  // needs per-tile sums before the PV product, which the MFMA sums cannot
+  // give in time; instead a P that overflowed fp16 makes its row's final
+  // sum inf (or NaN), the workgroup votes, and if any row failed it recomputes
+  // everything with the per-tile checked pass.  On inputs whose scores never
+  // exceed the first tile's max by ~16/c in a row (e.g. the N(0, 1)
+  // benchmark inputs) the second pass never runs.
+  constexpr bool kMfmaSums = !kUnroundedSum && !CAUSAL;
   static_assert(ITERS >= 1 && T::BYTES % (1024 * NW) == 0, "tile must split evenly over waves");
 
   // LDS ring: K buffers 0/1 then V buffers 0/1.
   __shared__ __attribute__((aligned(1024))) char smem[4 * T::BYTES];
+  // Set by any wave whose optimistic pass left a row with a non-finite sum.
+  __shared__ int redo_flag;
+  if (kMfmaSums && threadIdx.x == 0) redo_flag = 0;  // ordered by the first barrier
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -226,6 +243,8 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
   float m_run = -INFINITY;  // offset used in the exponent (<= the running max)
   float neg_mc = INFINITY;  // -m_run * c; +inf while m_run = -inf (trips the first check)
   float l_run = 0.0f;       // this lane's partial sum of P
+  f32x4 l_mfma = {0.0f, 0.0f, 0.0f, 0.0f};  // row sums on the matrix core (kMfmaSums)
+  const f16x8 sum_sel = row_sum_selector(lane);
 
   // Per-lane LDS byte offsets inside a tile (loop invariant).
   // K: A operand of key block kb, k-step kk -> row kb*32 + l32, chunk 2kk+g.
@@ -250,8 +269,13 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
-  auto compute_tile = [&](auto buf_c, int t) FA_INLINE {
+  // OPT: the optimistic pass of kMfmaSums kernels (offset from the first
+  // tile only, row sums on the matrix core); otherwise every tile checks its
+  // P sums before the PV product.
+  auto compute_tile = [&](auto buf_c, int t, auto opt_c) FA_INLINE {
     constexpr int BUF = decltype(buf_c)::value;
+    constexpr bool OPT = decltype(opt_c)::value;
+    static_assert(!OPT || kMfmaSums, "the optimistic pass needs the matrix-core sums");
     const int kt0 = t * BN;
     const char* kt = smem + BUF * T::BYTES;
 
@@ -338,7 +362,7 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
           }
         }
         pf[ch] = __builtin_bit_cast(i16x8, w);
-        if constexpr (!kUnroundedSum) {
+        if constexpr (!kUnroundedSum && !OPT) {
           // fp16, D = 128: sum the rounded P (the values that enter P V;
           // relative error <= 2^-11 per term) with v_dot2c_f32_f16.
           t0 = dot2_acc<BF16>(w[0], t0);
@@ -360,7 +384,15 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
     // ~15/c.  Then m moves to the row max for rows whose max exceeds it by
     // more than kRescaleThreshold (each row that tripped the check does), O
     // and l are rescaled, and P is recomputed.
-    if (__any(!(t0 + t1 < kSumLimit))) {
+    bool rederive;
+    if constexpr (OPT) {
+      rederive = t == 0;  // the first tile of every wave (it is never skipped)
+    } else {
+      rederive = __any(!(t0 + t1 < kSumLimit));
+    }
+    if (rederive) {
+      // (In the optimistic pass this is the first tile: O and the sums are
+      // still 0, so the rescale below is a no-op for them.)
       const float mx = pair_max(max32(s[0], s[1]));
       const bool grow = (mx - m_run) * c > kRescaleThreshold;  // false for NaN (-inf - -inf)
       const float m_new = grow ? mx : m_run;
@@ -379,7 +411,7 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
       neg_mc = none ? INFINITY : -m_run * c;
       exp_pack(none ? 0.0f : neg_mc);
     }
-    l_run += t0 + t1;
+    if constexpr (!OPT) l_run += t0 + t1;
 
     // ---- O^T += V^T P^T ----
     // Raised wave priority while this wave issues its PV MFMAs: the other
@@ -391,6 +423,7 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
       constexpr int j = decltype(j_c)::value;
       constexpr int db = j % DBLK, ch = j / DBLK;
       o_acc[db] = Ops::mfma(va[j % VD], pf[ch], o_acc[db]);
+      if constexpr (OPT && db == DBLK - 1) l_mfma = row_sum_mfma(sum_sel, pf[ch], l_mfma);
       if constexpr (j + VD < NPV) {
         constexpr int db2 = (j + VD) % DBLK, ch2 = (j + VD) / DBLK;
         constexpr int off = (2 + BUF) * T::BYTES + ch2 * 16 * T::ROWB;
@@ -401,22 +434,49 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
     __builtin_amdgcn_s_setprio(0);
   };
 
-  auto tile_step = [&](auto buf_c, int t) FA_INLINE {
+  auto tile_step = [&](auto buf_c, int t, auto opt_c) FA_INLINE {
     constexpr int BUF = decltype(buf_c)::value;
     if (t + 1 < n_tiles) issue_tile(t + 1, BUF ^ 1);
     // Skip tiles whose every key lies after every row of this wave.
-    if (!CAUSAL || t * BN <= wrow0 + 31) compute_tile(buf_c, t);
+    if (!CAUSAL || t * BN <= wrow0 + 31) compute_tile(buf_c, t, opt_c);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   };
+  auto run_tiles = [&](auto opt_c) FA_INLINE {
+    for (int t = 0; t < n_tiles; t += 2) {
+      tile_step(std::integral_constant<int, 0>{}, t, opt_c);
+      if (t + 1 < n_tiles) tile_step(std::integral_constant<int, 1>{}, t + 1, opt_c);
+    }
+  };
 
-  for (int t = 0; t < n_tiles; t += 2) {
-    tile_step(std::integral_constant<int, 0>{}, t);
-    if (t + 1 < n_tiles) tile_step(std::integral_constant<int, 1>{}, t + 1);
+  float l_tot;
+  if constexpr (kMfmaSums) {
+    run_tiles(std::true_type{});
+    l_tot = row_sum_of_lane(l_mfma, lane);
+    // Vote: did any row of the workgroup overflow?  (The loop ended with a
+    // barrier, so every wave is done with the K/V ring.)
+    if (__any(!(l_tot < INFINITY)) && lane == 0) redo_flag = 1;
+    __syncthreads();
+    if (redo_flag != 0) {
+#pragma unroll
+      for (int db = 0; db < DBLK; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o_acc[db][i] = 0.0f;
+      m_run = -INFINITY;
+      neg_mc = INFINITY;
+      l_run = 0.0f;
+      issue_tile(0, 0);
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      run_tiles(std::false_type{});
+      l_tot = pair_sum(l_run);
+    }
+  } else {
+    run_tiles(std::false_type{});
+    l_tot = pair_sum(l_run);
   }
 
-  // ---- epilogue: combine the two half-row partial sums, normalise, store ----
-  const float l_tot = pair_sum(l_run);
+  // ---- epilogue: normalise, store ----
   const bool row_ok = qrow < N;
   const float inv_l = (row_ok && l_tot > 0.0f) ? 1.0f / l_tot : 0.0f;
   if (row_ok) {

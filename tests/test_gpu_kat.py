@@ -27,6 +27,7 @@ def kat():
     L.kat_pair.argtypes = [fp, fp, fp]
     L.kat_dma.argtypes = [ctypes.POINTER(ctypes.c_int32)]
     L.kat_xcd_remap.argtypes = [ctypes.c_int, ctypes.POINTER(ctypes.c_int32)]
+    L.kat_row_sum.argtypes = [u16p, fp]
     return L
 
 
@@ -187,3 +188,21 @@ def test_xcd_remap_is_contiguous_per_xcd(kat, total):
         prev_hi = ids[-1]
         # consecutive dispatches on one XCD walk its range in order
         assert np.all(np.diff(out[np.arange(total) % 8 == x]) == 1)
+
+
+def test_row_sum_mfma_lane_map(kat):
+    """row_sum_mfma: the 16x16x32 MFMA with the selector operand sums each
+    query row's keys of a P^T chunk (lane l: row l % 32, key half l / 32),
+    and row_sum_of_lane hands every lane its row's total."""
+    print("case row_sum_mfma", flush=True)
+    rng = np.random.default_rng(9)
+    vals = rng.uniform(0.0, 4.0, size=(2, 64, 8)).astype(np.float16)
+    bits = np.ascontiguousarray(vals.view(np.uint16))
+    out = np.zeros(64, np.float32)
+    u16p = ctypes.POINTER(ctypes.c_uint16)
+    fp = ctypes.POINTER(ctypes.c_float)
+    assert kat.kat_row_sum(bits.ctypes.data_as(u16p), out.ctypes.data_as(fp)) == 0
+    per_lane = vals.astype(np.float64).sum(axis=(0, 2))      # both chunks, 8 keys
+    rows = per_lane[:32] + per_lane[32:]                      # the two key halves
+    expect = np.concatenate([rows, rows])
+    assert np.allclose(out, expect, rtol=1e-6, atol=1e-4), (out[:8], expect[:8])

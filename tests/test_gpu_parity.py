@@ -140,6 +140,20 @@ def test_score_jumps_vs_oracle(fa, oracle, pattern, causal, dtype):
     _check_against_oracle(oracle, q, k, v, o, lse, causal, scale, dtype, contract=False)
 
 
+@pytest.mark.parametrize("pattern", ["jump", "ramp", "drop"])
+def test_score_jumps_wide_workgroup_vs_oracle(fa, oracle, pattern):
+    """The same score jumps on the 8-wave workgroup (non-causal, N >= 2048):
+    the optimistic pass of fp16 D=128 overflows on "jump" and "ramp", and the
+    workgroup is recomputed with per-tile checks."""
+    _note(f"case jumps wide pattern={pattern}")
+    N, D = 2304, 128
+    q, k, v = make_qkv(1, 2, N, D, "fp16", seed=case_seed(778), device="cpu")
+    k = _scale_keys(k, pattern).to(torch.float16)
+    scale = 1.0 / math.sqrt(D)
+    o, lse = _fwd(fa, q.to(DEV), k.to(DEV), v.to(DEV), False)
+    _check_against_oracle(oracle, q, k, v, o, lse, False, scale, "fp16", contract=False)
+
+
 @pytest.mark.parametrize("case", range(24))
 def test_random_problems_vs_oracle(fa, oracle, case):
     """Seeded random problems: shape, dtype, mask, scale and memory layout
