@@ -78,3 +78,15 @@ def test_profile_cli_usage():
                 ["1x2x3"], ["a", "b"]):
         r = subprocess.run([PROFILE, *bad], capture_output=True, text=True, timeout=60)
         assert r.returncode == 1, bad
+
+
+PROBE = os.path.join(REPO, "flash-attention_amd", "flash_attention_runtime", "fa_mfma_probe")
+
+
+def test_mfma_probe_cli_rejects_bad_arguments():
+    """fa_mfma_probe validates its arguments before it touches a GPU."""
+    for bad in (["--ms", "0"], ["--ms", "abc"], ["--ms", "5000"], ["--rounds", "0"], ["--bogus"],
+                ["--ms"]):
+        r = subprocess.run([PROBE, *bad], capture_output=True, text=True, timeout=60)
+        assert r.returncode == 2, (bad, r.stdout, r.stderr)
+        assert "usage" in r.stderr or "must be" in r.stderr
