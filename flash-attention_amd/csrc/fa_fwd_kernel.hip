@@ -27,8 +27,8 @@
 //    (ds_read_b128) and the V transposed reads hit distinct banks.
 //  * LDS operands are read a few MFMAs ahead of use (K: 3 k-steps, V: 4
 //    MFMAs, the first V reads overlapping the softmax) so each MFMA finds its
-//    operand ready, and the wave issuing PV MFMAs runs at raised priority so
-//    the other wave on its SIMD fills the VALU with its softmax meanwhile.
+//    operand ready, and wave priorities keep the two waves of a SIMD in
+//    complementary phases (one wave's MFMAs while the other's softmax).
 //  * Causal: fully-masked K tiles are never loaded or computed; q-tiles are
 //    dispatched longest-first.  Ragged N: loads clamp to the last row and the
 //    scores of keys >= N are -inf; rows >= N are never stored.
@@ -150,6 +150,13 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  // Wave priorities.  8-wave workgroups: waves 4..7 (the second wave of each
+  // SIMD) run at raised priority throughout, so when both waves of a SIMD
+  // have MFMAs ready one of them streams ahead and the two drift into
+  // complementary phases (+0.6..1 % over the per-phase scheme at
+  // B4 H32 N4096).  4-wave workgroups, whose SIMD partner belongs to another
+  // workgroup, raise the priority only while issuing PV MFMAs (below).
+  if (NW == 8 && wave >= 4) __builtin_amdgcn_s_setprio(1);
   const int l32 = lane & 31;
   const int g = lane >> 5;         // which half of the wave
   const int lj = lane & 15;        // lane within its 16-lane group
@@ -414,10 +421,10 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
     if constexpr (!OPT) l_run += t0 + t1;
 
     // ---- O^T += V^T P^T ----
-    // Raised wave priority while this wave issues its PV MFMAs: the other
-    // wave on the SIMD is then usually in its softmax (VALU), and the
-    // arbiter keeps the matrix pipe fed from this one.
-    __builtin_amdgcn_s_setprio(1);
+    // 4-wave workgroups: raised wave priority while this wave issues its PV
+    // MFMAs: the other wave on the SIMD is then usually in its softmax
+    // (VALU), and the arbiter keeps the matrix pipe fed from this one.
+    if constexpr (NW != 8) __builtin_amdgcn_s_setprio(1);
     __builtin_amdgcn_sched_barrier(0);
     static_for<0, NPV>([&](auto j_c) {
       constexpr int j = decltype(j_c)::value;
@@ -431,7 +438,7 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
       }
       __builtin_amdgcn_sched_barrier(0);
     });
-    __builtin_amdgcn_s_setprio(0);
+    if constexpr (NW != 8) __builtin_amdgcn_s_setprio(0);
   };
 
   auto tile_step = [&](auto buf_c, int t, auto opt_c) FA_INLINE {
