@@ -7,8 +7,8 @@
 //
 //  * One workgroup = NW wave64s, each wave owns 32 query rows (BM = 32*NW):
 //    NW = 4 with two workgroups per CU, or NW = 8 (one workgroup per CU,
-//    half the staging traffic per flop) for long non-causal rows; either
-//    way two waves share each SIMD.
+//    half the staging traffic per flop) for long rows (non-causal N >= 2048,
+//    causal fp16 N >= 8192); either way two waves share each SIMD.
 //  * S^T = K * Q^T on v_mfma_f32_32x32x16_{f16,bf16}: K tile rows are the A
 //    operand (read from LDS), Q rows are the B operand (kept in VGPRs for the
 //    whole kernel).  In the 32x32 accumulator layout lane l holds column
@@ -110,8 +110,10 @@ constexpr float kRescaleThreshold = 8.0f;
 constexpr int kKWindow = 3;
 constexpr int kVWindow = 4;
 
-// Non-causal problems with at least this many keys use 8-wave workgroups.
+// Non-causal problems with at least this many keys use 8-wave workgroups;
+// causal fp16 problems from kWideCausalMinSeq keys on.
 constexpr int kWideMinSeq = 2048;
+constexpr int kWideCausalMinSeq = 8192;
 
 template <int D, bool BF16, bool CAUSAL, int NW>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
@@ -128,9 +130,10 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
   // issue faster than one v_dot2c_f32_f16 (+8 % at B4 H16 N1024 D64);
   // fp16 at D = 128 sums the rounded P (v_dot2c, or the matrix core below).
   constexpr bool kUnroundedSum = BF16 || D == 64;
-  // fp16, D = 128, non-causal: the rounded-P row sums run on the matrix core
-  // (row_sum_mfma, 4 small MFMAs per tile in place of 16 v_dot2c; +3 % at
-  // B4 H32 N4096, neutral for the causal kernels, which keep v_dot2c), and the
+  // fp16, D = 128, 8-wave or non-causal: the rounded-P row sums run on the
+  // matrix core (row_sum_mfma, 4 small MFMAs per tile in place of 16 v_dot2c;
+  // +3 % at B4 H32 N4096, +2.7 % at causal B1 H16 N16384; neutral for the
+  // 4-wave causal kernel, which keeps v_dot2c), and the
   // kernel runs an optimistic pass first: the offset m is taken from the row
   // max of the first key tile only and never checked again.  The check
   // needs per-tile sums before the PV product, which the MFMA sums cannot
@@ -139,7 +142,7 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
   // everything with the per-tile checked pass.  On inputs whose scores never
   // exceed the first tile's max by ~16/c in a row (e.g. the N(0, 1)
   // benchmark inputs) the second pass never runs.
-  constexpr bool kMfmaSums = !kUnroundedSum && !CAUSAL;
+  constexpr bool kMfmaSums = !kUnroundedSum && (!CAUSAL || NW == 8);
   static_assert(ITERS >= 1 && T::BYTES % (1024 * NW) == 0, "tile must split evenly over waves");
 
   // LDS ring: K buffers 0/1 then V buffers 0/1.
@@ -518,7 +521,14 @@ hipError_t launch_one(const KernelArgs& a, hipStream_t stream) {
 
 template <int D, bool BF16>
 hipError_t launch_causal(const KernelArgs& a, hipStream_t stream) {
-  if (a.causal) return launch_one<D, BF16, true, 4>(a, stream);
+  if (a.causal) {
+    // Long causal fp16 rows: 8-wave workgroups (+1.4 % at B1 H16 N16384,
+    // +4 % with the matrix-core row sums they enable); bf16 measured neutral
+    // and short problems lose (-11 % at N = 3000: fewer, longer workgroups).
+    if constexpr (!BF16)
+      if (a.seq_len >= kWideCausalMinSeq) return launch_one<D, BF16, true, 8>(a, stream);
+    return launch_one<D, BF16, true, 4>(a, stream);
+  }
   // Long non-causal rows: 8 waves (BM = 256) per workgroup, one workgroup
   // per CU, halve the L2->LDS tile traffic per flop; the chip is power
   // limited there and the saved data movement buys clock (measured +3 % at

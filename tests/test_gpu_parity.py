@@ -293,6 +293,36 @@ def test_config_sampled_rows_vs_oracle(fa, oracle, name):
     assert bool((of >= vmin - margin).all().item()), "O below the convex hull of V"
 
 
+@pytest.mark.parametrize("pattern", ["ramp", "drop"])
+def test_score_jumps_long_causal_sampled_rows(fa, oracle, pattern):
+    """Causal fp16 at N = 8192 runs 8-wave workgroups with the optimistic pass;
+    "ramp" keys make late scores overflow the first tile's offset, so the
+    workgroups redo the work with per-tile checks.  Sampled rows against the
+    fp64 oracle and the reference-kernel emulator."""
+    _note(f"case jumps long causal pattern={pattern}")
+    N, D = 8192, 128
+    q, k, v = make_qkv(1, 2, N, D, "fp16", seed=case_seed(779), device="cpu")
+    k = _scale_keys(k, pattern).to(torch.float16)
+    scale = 1.0 / math.sqrt(D)
+    o, lse = _fwd(fa, q.to(DEV), k.to(DEV), v.to(DEV), True)
+    rng = np.random.default_rng(779)
+    heads, sel_bh, sel_row = _sample_rows(N, 2, rng, n_random=32)
+    qn, kn, vn = to_np32(q), to_np32(k), to_np32(v)
+    ref_o, ref_lse = oracle.attn_rows_f64(qn, kn, vn, scale, True, sel_bh, sel_row)
+    emu_o, _ = oracle.kernel_numerics_rows(qn, kn, vn, scale, True, sel_bh, sel_row, oracle.F16)
+    got_o = to_np32(o.reshape(2, N, D).cpu())[sel_bh, sel_row]
+    got_lse = to_np32(lse.reshape(2, N).cpu())[sel_bh, sel_row]
+    mx, mean = err_stats(got_o, ref_o)
+    emx, emean = err_stats(emu_o, ref_o)
+    lse_err = float(np.abs(got_lse.astype(np.float64) - ref_lse).max())
+    _note(f"  sampled {len(sel_row)} rows: max_abs={mx:.3e} mean_abs={mean:.3e} "
+          f"(ref-kernel emu {emx:.3e}/{emean:.3e}) lse={lse_err:.3e}")
+    assert np.isfinite(got_o).all()
+    assert mx <= MAX_ABS_TOL
+    assert mx <= 3 * emx + 1e-6 and mean <= 2 * emean + 1e-6
+    assert lse_err <= LSE_TOL
+
+
 @pytest.mark.parametrize("causal", [False, True], ids=["noncausal", "causal"])
 def test_long_sequence_sampled_rows(fa, oracle, causal):
     """N = 32768 (beyond every BASELINE config): sampled rows against the
