@@ -125,15 +125,16 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
   constexpr int KSTEPS = D / 16;  // MFMA k-steps for S^T (k = head dim)
   constexpr int DBLK = D / 32;    // 32-wide head-dim blocks of O^T
   constexpr int ITERS = T::BYTES / (1024 * NW);  // DMA instructions per wave per tile
-  // Row sums of P: fp32 sums of the unrounded p for bf16, and for fp16 at
-  // D = 64, where the softmax is twice as dense per MFMA and two v_add_f32
-  // issue faster than one v_dot2c_f32_f16 (+8 % at B4 H16 N1024 D64);
-  // fp16 at D = 128 sums the rounded P (v_dot2c, or the matrix core below).
+  // Row sums of P in the per-tile checked pass: fp32 sums of the unrounded p
+  // for bf16, and for fp16 at D = 64, where the softmax is twice as dense per
+  // MFMA and two v_add_f32 issue faster than one v_dot2c_f32_f16 (+8 % at
+  // B4 H16 N1024 D64); fp16 at D = 128 sums the rounded P with v_dot2c.
   constexpr bool kUnroundedSum = BF16 || D == 64;
-  // fp16, D = 128, 8-wave or non-causal: the rounded-P row sums run on the
-  // matrix core (row_sum_mfma, 4 small MFMAs per tile in place of 16 v_dot2c;
-  // +3 % at B4 H32 N4096, +2.7 % at causal B1 H16 N16384; neutral for the
-  // 4-wave causal kernel, which keeps v_dot2c), and the
+  // fp16, 8-wave or non-causal: the row sums of the rounded P run on the
+  // matrix core (row_sum_mfma, 4 small MFMAs per tile in place of 16 v_dot2c
+  // or 32 v_add_f32; +3 % at B4 H32 N4096, +2.7 % at causal B1 H16 N16384,
+  // +4 % at B4 H16 N1024 D64; neutral for the 4-wave causal kernel, which
+  // keeps the checked pass), and the
   // kernel runs an optimistic pass first: the offset m is taken from the row
   // max of the first key tile only and never checked again.  The check
   // needs per-tile sums before the PV product, which the MFMA sums cannot
@@ -142,7 +143,7 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
   // everything with the per-tile checked pass.  On inputs whose scores never
   // exceed the first tile's max by ~16/c in a row (e.g. the N(0, 1)
   // benchmark inputs) the second pass never runs.
-  constexpr bool kMfmaSums = !kUnroundedSum && (!CAUSAL || NW == 8);
+  constexpr bool kMfmaSums = !BF16 && (!CAUSAL || NW == 8);
   static_assert(ITERS >= 1 && T::BYTES % (1024 * NW) == 0, "tile must split evenly over waves");
 
   // LDS ring: K buffers 0/1 then V buffers 0/1.
@@ -363,7 +364,7 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
           const float p0 = fast_exp2(fmaf(s[kb][base + 2 * j], c, nmc));
           const float p1 = fast_exp2(fmaf(s[kb][base + 2 * j + 1], c, nmc));
           w[j] = pack2<BF16>(p0, p1);
-          if constexpr (kUnroundedSum) {
+          if constexpr (kUnroundedSum && !OPT) {
             // Sum the unrounded fp32 p, as the reference does
             // (online_softmax.cuh:135-152).  bf16 needs it: its 8
             // significant bits would cost up to 2^-9 in the LSE.
