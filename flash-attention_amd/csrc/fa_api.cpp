@@ -11,6 +11,7 @@
 // launched.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdint>
@@ -92,6 +93,81 @@ void to_kernel_args(const fa_fwd_params* p, fa::KernelArgs* a) {
   a->scale = p->softmax_scale;
   // c = scale * log2(e) (reference: src/config/config.cuh:84, forward_v6_mma.cuh:375)
   a->scale_log2 = p->softmax_scale * 1.4426950408889634f;
+  a->ws_o = nullptr;
+  a->ws_ml = nullptr;
+  a->split.n_items = 0;
+  a->split.n_slots = 0;
+  a->split.n_merge = 0;
+}
+
+// Compute units of the calling thread's current device.
+fa_status current_compute_units(int* cus) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e == hipSuccess) e = hipDeviceGetAttribute(cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e != hipSuccess)
+    return fail(FA_ERR_HIP, "device query failed: %s", hipGetErrorString(e));
+  return FA_OK;
+}
+
+// Validates p and launches it, split over the workspace when the plan for
+// the current device asks for one and a workspace is given (workspace ==
+// NULL: never split, the plain fa_fwd path).
+fa_status launch(const fa_fwd_params* p, void* workspace, uint64_t workspace_bytes,
+                 void* stream) {
+  const fa_status s = fa_fwd_validate(p);
+  if (s != FA_OK) return s;
+  fa::KernelArgs a;
+  to_kernel_args(p, &a);
+  if (workspace != nullptr) {
+    int cus = 0;
+    const fa_status st = current_compute_units(&cus);
+    if (st != FA_OK) return st;
+    const size_t need = fa::plan_split(a, cus, &a.split);
+    if (need > 0) {
+      if (workspace_bytes < need)
+        return fail(FA_ERR_ARG, "workspace of %llu bytes is smaller than the %llu bytes needed",
+                    (unsigned long long)workspace_bytes, (unsigned long long)need);
+      if (!aligned16(workspace))
+        return fail(FA_ERR_STRIDE, "workspace pointer is not 16-byte aligned");
+      const size_t o_bytes = (size_t)p->batch * p->heads * a.split.n_slots *
+                             fa::block_rows(a) * p->head_dim * 4;
+      a.ws_o = static_cast<float*>(workspace);
+      a.ws_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) + o_bytes);
+    }
+  }
+  const hipError_t e = fa::launch_fwd(a, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess)
+    return fail(FA_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(e));
+  return FA_OK;
+}
+
+// launch() bracketed by two HIP events on `stream`.
+fa_status launch_timed(const fa_fwd_params* p, void* workspace, uint64_t workspace_bytes,
+                       void* stream, float* ms) {
+  if (ms == nullptr) return fail(FA_ERR_NULL, "ms is NULL");
+  *ms = 0.0f;
+  const fa_status s = fa_fwd_validate(p);
+  if (s != FA_OK) return s;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipEvent_t start = nullptr, stop = nullptr;
+  hipError_t e = hipEventCreate(&start);
+  if (e == hipSuccess) e = hipEventCreate(&stop);
+  if (e == hipSuccess) e = hipEventRecord(start, st);
+  fa_status out = FA_OK;
+  if (e == hipSuccess) {
+    out = launch(p, workspace, workspace_bytes, stream);
+    if (out == FA_OK) {
+      e = hipEventRecord(stop, st);
+      if (e == hipSuccess) e = hipEventSynchronize(stop);
+      if (e == hipSuccess) e = hipEventElapsedTime(ms, start, stop);
+    }
+  }
+  if (start) (void)hipEventDestroy(start);
+  if (stop) (void)hipEventDestroy(stop);
+  if (out != FA_OK) return out;
+  if (e != hipSuccess) return fail(FA_ERR_HIP, "event timing failed: %s", hipGetErrorString(e));
+  return FA_OK;
 }
 
 }  // namespace
@@ -155,40 +231,91 @@ fa_status fa_fwd_validate(const fa_fwd_params* p) {
 }
 
 fa_status fa_fwd(const fa_fwd_params* p, void* stream) {
-  const fa_status s = fa_fwd_validate(p);
-  if (s != FA_OK) return s;
-  fa::KernelArgs a;
-  to_kernel_args(p, &a);
-  const hipError_t e = fa::launch_fwd(a, static_cast<hipStream_t>(stream));
-  if (e != hipSuccess)
-    return fail(FA_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(e));
-  return FA_OK;
+  return launch(p, nullptr, 0, stream);
 }
 
 fa_status fa_fwd_timed(const fa_fwd_params* p, void* stream, float* ms) {
-  if (ms == nullptr) return fail(FA_ERR_NULL, "ms is NULL");
-  *ms = 0.0f;
+  return launch_timed(p, nullptr, 0, stream, ms);
+}
+
+fa_status fa_fwd_plan(const fa_fwd_params* p, int32_t compute_units, fa_fwd_plan_t* out) {
+  if (out == nullptr) return fail(FA_ERR_NULL, "out is NULL");
+  std::memset(out, 0, sizeof(*out));
   const fa_status s = fa_fwd_validate(p);
   if (s != FA_OK) return s;
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  hipEvent_t start = nullptr, stop = nullptr;
-  hipError_t e = hipEventCreate(&start);
-  if (e == hipSuccess) e = hipEventCreate(&stop);
-  if (e == hipSuccess) e = hipEventRecord(start, st);
-  fa_status out = FA_OK;
-  if (e == hipSuccess) {
-    out = fa_fwd(p, stream);
-    if (out == FA_OK) {
-      e = hipEventRecord(stop, st);
-      if (e == hipSuccess) e = hipEventSynchronize(stop);
-      if (e == hipSuccess) e = hipEventElapsedTime(ms, start, stop);
+  if (compute_units < 1)
+    return fail(FA_ERR_ARG, "compute_units must be >= 1 (got %d)", (int)compute_units);
+  fa::KernelArgs a;
+  to_kernel_args(p, &a);
+  out->workspace_bytes = fa::plan_split(a, compute_units, &a.split);
+  out->block_rows = fa::block_rows(a);
+  out->n_items = a.split.n_items;
+  out->n_slots = a.split.n_slots;
+  out->n_merge = a.split.n_merge;
+  for (int i = 0; i < a.split.n_items; ++i) {
+    const uint32_t info = a.split.item[i];
+    const int qb = (int)(info & 0xffffu), c = (int)((info >> 16) & 0xffu), nch = (int)(info >> 24);
+    // The kernel's split of the q-tile's key tiles [0, T) (fa_fwd_kernel).
+    const int kv = p->causal ? std::min(p->seq_len, (qb + 1) * out->block_rows) : p->seq_len;
+    const int T = (kv + 63) / 64;
+    out->q_tile[i] = qb;
+    out->n_chunks[i] = nch;
+    out->tile_begin[i] = (int32_t)((int64_t)c * T / nch);
+    out->tile_end[i] = (int32_t)((int64_t)(c + 1) * T / nch);
+    out->slot[i] = nch > 1 ? a.split.slot[i] + c : -1;
+  }
+  return FA_OK;
+}
+
+fa_status fa_fwd_workspace_size(const fa_fwd_params* p, uint64_t* bytes) {
+  if (bytes == nullptr) return fail(FA_ERR_NULL, "bytes is NULL");
+  *bytes = 0;
+  const fa_status s = fa_fwd_validate(p);
+  if (s != FA_OK) return s;
+  int cus = 0;
+  const fa_status st = current_compute_units(&cus);
+  if (st != FA_OK) return st;
+  fa::KernelArgs a;
+  to_kernel_args(p, &a);
+  *bytes = fa::plan_split(a, cus, &a.split);
+  return FA_OK;
+}
+
+fa_status fa_fwd_ws(const fa_fwd_params* p, void* workspace, uint64_t workspace_bytes,
+                    void* stream) {
+  if (workspace == nullptr && workspace_bytes != 0)
+    return fail(FA_ERR_NULL, "workspace is NULL but workspace_bytes = %llu",
+                (unsigned long long)workspace_bytes);
+  if (workspace == nullptr) {
+    // Allowed only when the problem needs no workspace.
+    uint64_t need = 0;
+    const fa_status s = fa_fwd_workspace_size(p, &need);
+    if (s != FA_OK) return s;
+    if (need > 0)
+      return fail(FA_ERR_NULL, "workspace is NULL but %llu bytes are needed",
+                  (unsigned long long)need);
+  }
+  return launch(p, workspace, workspace_bytes, stream);
+}
+
+fa_status fa_fwd_ws_timed(const fa_fwd_params* p, void* workspace, uint64_t workspace_bytes,
+                          void* stream, float* ms) {
+  if (workspace == nullptr && workspace_bytes != 0) {
+    if (ms != nullptr) *ms = 0.0f;
+    return fail(FA_ERR_NULL, "workspace is NULL but workspace_bytes = %llu",
+                (unsigned long long)workspace_bytes);
+  }
+  if (workspace == nullptr) {
+    uint64_t need = 0;
+    const fa_status s = fa_fwd_workspace_size(p, &need);
+    if (s != FA_OK) return s;
+    if (need > 0) {
+      if (ms != nullptr) *ms = 0.0f;
+      return fail(FA_ERR_NULL, "workspace is NULL but %llu bytes are needed",
+                  (unsigned long long)need);
     }
   }
-  if (start) (void)hipEventDestroy(start);
-  if (stop) (void)hipEventDestroy(stop);
-  if (out != FA_OK) return out;
-  if (e != hipSuccess) return fail(FA_ERR_HIP, "event timing failed: %s", hipGetErrorString(e));
-  return FA_OK;
+  return launch_timed(p, workspace, workspace_bytes, stream, ms);
 }
 
 fa_status fa_device_info(int device, fa_device_info_t* out) {

@@ -1,13 +1,35 @@
 // Internal interface between the C ABI (fa_api.cpp) and the HIP kernels.
 // Mirrors the reference's kernel argument block ForwardKernelArgs
-// (src/config/config.cuh:20-45) with 64-bit strides, dtype, LSE and the
-// precomputed exponent scale.
+// (src/config/config.cuh:20-45) with 64-bit strides, dtype, LSE, the
+// precomputed exponent scale and the split-KV work plan.
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <stddef.h>
 #include <stdint.h>
 
 namespace fa {
+
+// Split-KV: long key ranges of a q-tile are cut into chunks computed by
+// separate workgroups, whose partial results (unnormalised fp32 O, offset m
+// and row sum l per row) go to a caller-provided workspace and are merged by
+// a second kernel.  Used when the grid would leave most of the machine idle
+// behind a few long q-tiles (short causal problems, few heads).
+constexpr int kMaxSplitItems = 128;
+
+struct SplitPlan {
+  int32_t n_items;   // work items per (batch, head); 0: no split
+  int32_t n_slots;   // partial-result slots per (batch, head)
+  int32_t n_merge;   // q-tiles with more than one chunk (merged by the second kernel)
+  // Item i: q-tile (bits 0..15), chunk (16..23), chunk count (24..31).
+  uint32_t item[kMaxSplitItems];
+  // Item i's first partial slot of its q-tile (items of one q-tile use
+  // slot[i] + chunk); unused for single-chunk items.
+  uint16_t slot[kMaxSplitItems];
+  // Merge list: q-tile (bits 0..15) | chunk count (16..23), first slot in merge_slot.
+  uint32_t merge[kMaxSplitItems];
+  uint16_t merge_slot[kMaxSplitItems];
+};
 
 struct KernelArgs {
   const void* q;
@@ -26,9 +48,22 @@ struct KernelArgs {
   int32_t n_qblocks;  // filled by the launcher
   float scale;        // softmax scale (natural units, used for the LSE)
   float scale_log2;   // softmax scale * log2(e), used for exp2
+  // Split-KV (filled by the launcher when a workspace is used).
+  float* ws_o;        // [batch*heads][n_slots][BM][head_dim] fp32 partial O
+  float* ws_ml;       // [batch*heads][n_slots][BM][2] fp32 (m, l)
+  SplitPlan split;
 };
 
+// Workgroup rows (BM) of the kernel variant launch_fwd picks for args.
+int block_rows(const KernelArgs& args);
+
+// Computes the split plan for args on a device with `compute_units` CUs.
+// Returns the workspace bytes it needs (0: no split; plan->n_items = 0).
+size_t plan_split(const KernelArgs& args, int compute_units, SplitPlan* plan);
+
 // Launches the forward kernel for args (validated by the caller) on stream.
+// With args.split.n_items > 0 (and the workspace set) it launches the split
+// kernel and the merge kernel.
 hipError_t launch_fwd(const KernelArgs& args, hipStream_t stream);
 
 }  // namespace fa

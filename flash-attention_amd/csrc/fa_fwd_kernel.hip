@@ -34,6 +34,10 @@
 //    scores of keys >= N are -inf; rows >= N are never stored.
 //  * Block ids are remapped so each XCD (private L2) works on consecutive
 //    q-tiles of the same heads.
+//  * Split-KV (with a caller workspace, when a few long q-tiles would set
+//    the time of a short grid): a q-tile's key tiles are cut into chunks
+//    computed by separate workgroups, which write fp32 partials (O, m, l);
+//    fa_merge_kernel combines them.
 //
 // Numerics follow the reference (src/softmax/online_softmax.cuh:13-19,
 // :89-152; src/forward/forward_v6_mma.cuh:19-38): fp32 scores, an exponent
@@ -43,16 +47,19 @@
 // normalised in fp32 and rounded to the input type.  Differences: m is an
 // offset at or below the running max, raised only when a tile's P would
 // reach 2^15 (the common factor exp2(m_max*c - m*c) cancels in O/l), so the
-// row max is computed only on such tiles (non-causal fp16 at D = 128 runs an
-// optimistic pass with the offset of the first tile and redoes the workgroup
-// with per-tile checks only if a P overflowed); fp16 at D = 128 sums the
-// rounded P into l (the weights P V actually uses), bf16 and fp16 at D = 64
-// the unrounded p as the reference; and the natural-log LSE = m*scale + ln(l)
-// is new.
+// row max is computed only on such tiles (fp16 non-causal and fp16 causal in
+// 8-wave workgroups run an optimistic pass with the offset of the first tile
+// and redo the workgroup with per-tile checks only if a P overflowed); l is
+// the sum of the rounded P (the weights P V actually uses) in the optimistic
+// pass and in the checked pass of fp16 at D = 128, and of the unrounded p,
+// as the reference, in the checked pass of bf16 and of fp16 at D = 64; and
+// the natural-log LSE = m*scale + ln(l) is new.
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
+#include <cmath>
 #include <type_traits>
 
 #include "fa_device_ops.h"
@@ -115,7 +122,9 @@ constexpr int kVWindow = 4;
 constexpr int kWideMinSeq = 2048;
 constexpr int kWideCausalMinSeq = 8192;
 
-template <int D, bool BF16, bool CAUSAL, int NW>
+// SPLIT: the grid runs the work items of args.split (chunks of q-tiles);
+// otherwise one workgroup per q-tile.
+template <int D, bool BF16, bool CAUSAL, int NW, bool SPLIT>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
     fa_fwd_kernel(const KernelArgs args) {
   using T = Tile<D>;
@@ -168,9 +177,20 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
 
   const int N = args.seq_len;
   const int logical = xcd_remap(blockIdx.x, gridDim.x);
-  const int bh = logical / args.n_qblocks;
-  int qb = logical - bh * args.n_qblocks;
-  if (CAUSAL) qb = args.n_qblocks - 1 - qb;  // longest q-tiles first
+  // Work item of this workgroup: a q-tile, or with split-KV one chunk of a
+  // q-tile's key tiles (the plan lists items longest first).
+  const int per_bh = SPLIT ? args.split.n_items : args.n_qblocks;
+  const int bh = logical / per_bh;
+  const int item = logical - bh * per_bh;
+  int qb, chunk = 0, n_chunks = 1;
+  if constexpr (SPLIT) {
+    const uint32_t info = args.split.item[item];
+    qb = (int)(info & 0xffffu);
+    chunk = (int)((info >> 16) & 0xffu);
+    n_chunks = (int)(info >> 24);
+  } else {
+    qb = CAUSAL ? args.n_qblocks - 1 - item : item;  // longest q-tiles first
+  }
   const int b = bh / args.heads;
   const int h = bh - b * args.heads;
 
@@ -189,7 +209,10 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
   const int wrow0 = q0 + wave * 32;  // first query row of this wave
   const int qrow = wrow0 + l32;      // this lane's query row
   const int kv_end = CAUSAL ? min(N, q0 + BM) : N;
-  const int n_tiles = (kv_end + BN - 1) / BN;
+  const int q_tiles = (kv_end + BN - 1) / BN;  // key tiles of this q-tile
+  // This item's key tiles [t_begin, t_end): chunk of n_chunks near-equal parts.
+  const int t_begin = (int)((int64_t)chunk * q_tiles / n_chunks);
+  const int t_end = (int)((int64_t)(chunk + 1) * q_tiles / n_chunks);
 
   // ---- DMA plan: per-lane 32-bit source offsets within a tile ----
   uint32_t k_src[ITERS], v_src[ITERS];
@@ -231,8 +254,8 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
     }
   };
 
-  // Start streaming tile 0 while Q is fetched into registers.
-  issue_tile(0, 0);
+  // Start streaming the first tile while Q is fetched into registers.
+  issue_tile(t_begin, 0);
 
   // Q as the B operand of S^T = K Q^T: lane holds query qrow, dims
   // [16*kk + 8*g, +8) for k-step kk.
@@ -397,7 +420,7 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
     // and l are rescaled, and P is recomputed.
     bool rederive;
     if constexpr (OPT) {
-      rederive = t == 0;  // the first tile of every wave (it is never skipped)
+      rederive = t == t_begin;  // the first tile of every wave that computes any
     } else {
       rederive = __any(!(t0 + t1 < kSumLimit));
     }
@@ -447,16 +470,16 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
 
   auto tile_step = [&](auto buf_c, int t, auto opt_c) FA_INLINE {
     constexpr int BUF = decltype(buf_c)::value;
-    if (t + 1 < n_tiles) issue_tile(t + 1, BUF ^ 1);
+    if (t + 1 < t_end) issue_tile(t + 1, BUF ^ 1);
     // Skip tiles whose every key lies after every row of this wave.
     if (!CAUSAL || t * BN <= wrow0 + 31) compute_tile(buf_c, t, opt_c);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   };
   auto run_tiles = [&](auto opt_c) FA_INLINE {
-    for (int t = 0; t < n_tiles; t += 2) {
+    for (int t = t_begin; t < t_end; t += 2) {
       tile_step(std::integral_constant<int, 0>{}, t, opt_c);
-      if (t + 1 < n_tiles) tile_step(std::integral_constant<int, 1>{}, t + 1, opt_c);
+      if (t + 1 < t_end) tile_step(std::integral_constant<int, 1>{}, t + 1, opt_c);
     }
   };
 
@@ -476,7 +499,7 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
       m_run = -INFINITY;
       neg_mc = INFINITY;
       l_run = 0.0f;
-      issue_tile(0, 0);
+      issue_tile(t_begin, 0);
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
       run_tiles(std::false_type{});
@@ -487,8 +510,29 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
     l_tot = pair_sum(l_run);
   }
 
-  // ---- epilogue: normalise, store ----
   const bool row_ok = qrow < N;
+  if (SPLIT && n_chunks > 1) {
+    // ---- split-KV partial: unnormalised O, offset m (raw score units; -inf
+    // when no key of this chunk is visible to the row) and row sum l ----
+    const int64_t slot = (int64_t)args.split.slot[item] + chunk;
+    const int64_t row = ((int64_t)bh * args.split.n_slots + slot) * BM + (qrow - q0);
+    if (row_ok) {
+      float* po = args.ws_o + row * D;
+#pragma unroll
+      for (int db = 0; db < DBLK; ++db)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int col = 32 * db + 8 * r + 4 * g;
+          const f32x4 w = {o_acc[db][4 * r + 0], o_acc[db][4 * r + 1], o_acc[db][4 * r + 2],
+                           o_acc[db][4 * r + 3]};
+          *reinterpret_cast<f32x4*>(po + col) = w;
+        }
+      if (g == 0) *reinterpret_cast<f32x2*>(args.ws_ml + row * 2) = f32x2{m_run, l_tot};
+    }
+    return;
+  }
+
+  // ---- epilogue: normalise, store ----
   const float inv_l = (row_ok && l_tot > 0.0f) ? 1.0f / l_tot : 0.0f;
   if (row_ok) {
     char* op = oh + qrow * osb;
@@ -508,15 +552,101 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
   }
 }
 
+// Split-KV merge: one thread per 4 head-dim elements of a row of a q-tile
+// with more than one chunk.  O = sum_c w_c O_c / sum_c w_c l_c with
+// w_c = exp2((m_c - m) * c) and m = max_c m_c (the single-pass online
+// softmax regrouped by chunk; chunks whose rows saw no key have l_c = 0 and
+// are skipped), LSE = m * scale + ln(l).  Chunks are read kMergeGroup at a
+// time with all loads issued together, so a row costs one memory latency
+// per group rather than one per chunk.
+constexpr int kMergeGroup = 4;
+
+template <int D, bool BF16>
+__global__ void __launch_bounds__(256) fa_merge_kernel(const KernelArgs args, int BM) {
+  constexpr int TPR = D / 4;       // threads per row
+  constexpr int RPB = 256 / TPR;   // rows per workgroup
+  const int per_tile = (BM + RPB - 1) / RPB;
+  const int per_bh = args.split.n_merge * per_tile;
+  const int bh = blockIdx.x / per_bh;
+  const int rem = blockIdx.x - bh * per_bh;
+  const int mi = rem / per_tile;
+  const int r = (rem - mi * per_tile) * RPB + (int)threadIdx.x / TPR;
+  const int d = ((int)threadIdx.x % TPR) * 4;
+  const uint32_t info = args.split.merge[mi];
+  const int qb = (int)(info & 0xffffu);
+  const int nch = (int)((info >> 16) & 0xffu);
+  const int q = qb * BM + r;
+  if (r >= BM || q >= args.seq_len) return;
+  // Rows < seq_len of every chunk were written (O = 0, l = 0 where no key
+  // was visible), so every load below reads written data.
+  const int64_t row0 = ((int64_t)bh * args.split.n_slots + args.split.merge_slot[mi]) * BM + r;
+  const float c2 = args.scale_log2;
+  float m = -INFINITY, l = 0.0f;
+  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int c0 = 0; c0 < nch; c0 += kMergeGroup) {
+    f32x2 ml[kMergeGroup];
+    f32x4 oc[kMergeGroup];
+#pragma unroll
+    for (int j = 0; j < kMergeGroup; ++j) {
+      const int64_t rc = row0 + (int64_t)min(c0 + j, nch - 1) * BM;
+      ml[j] = *reinterpret_cast<const f32x2*>(args.ws_ml + rc * 2);
+      oc[j] = *reinterpret_cast<const f32x4*>(args.ws_o + rc * D + d);
+    }
+    float mg = m;
+#pragma unroll
+    for (int j = 0; j < kMergeGroup; ++j)
+      if (c0 + j < nch && ml[j][1] > 0.0f) mg = fmaxf(mg, ml[j][0]);
+    if (l > 0.0f && mg > m) {
+      const float a = fast_exp2((m - mg) * c2);
+      l *= a;
+      acc *= a;
+    }
+    m = mg;
+#pragma unroll
+    for (int j = 0; j < kMergeGroup; ++j)
+      if (c0 + j < nch && ml[j][1] > 0.0f) {
+        const float w = fast_exp2((ml[j][0] - m) * c2);
+        l += w * ml[j][1];
+        acc += w * oc[j];
+      }
+  }
+  const float inv_l = l > 0.0f ? 1.0f / l : 0.0f;
+  const int b = bh / args.heads;
+  const int h = bh - b * args.heads;
+  char* op = reinterpret_cast<char*>(args.o) +
+             2 * (b * args.o_stride_b + h * args.o_stride_h + (int64_t)q * args.o_stride_s + d);
+  *reinterpret_cast<u32x2*>(op) = u32x2{pack2<BF16>(acc[0] * inv_l, acc[1] * inv_l),
+                                        pack2<BF16>(acc[2] * inv_l, acc[3] * inv_l)};
+  if (args.lse != nullptr && d == 0)
+    args.lse[(int64_t)bh * args.seq_len + q] = (m == -INFINITY ? 0.0f : m) * args.scale + __logf(l);
+}
+
 template <int D, bool BF16, bool CAUSAL, int NW>
 hipError_t launch_one(const KernelArgs& a, hipStream_t stream) {
   constexpr int BM = 32 * NW;
   KernelArgs args = a;
   args.n_qblocks = (args.seq_len + BM - 1) / BM;
-  const int64_t total = (int64_t)args.n_qblocks * args.batch * args.heads;
+  // A split plan is only valid for the block height it was made for.
+  if (args.split.n_items > 0 && (block_rows(args) != BM || args.ws_o == nullptr ||
+                                 args.ws_ml == nullptr || args.split.n_items > kMaxSplitItems))
+    return hipErrorInvalidValue;
+  const int64_t bh = (int64_t)args.batch * args.heads;
+  const int64_t total = (args.split.n_items > 0 ? args.split.n_items : args.n_qblocks) * bh;
   if (total > 0x7fffffff) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((fa_fwd_kernel<D, BF16, CAUSAL, NW>), dim3((unsigned)total), dim3(NW * 64),
-                     0, stream, args);
+  if (args.split.n_items == 0) {
+    hipLaunchKernelGGL((fa_fwd_kernel<D, BF16, CAUSAL, NW, false>), dim3((unsigned)total),
+                       dim3(NW * 64), 0, stream, args);
+    return hipGetLastError();
+  }
+  hipLaunchKernelGGL((fa_fwd_kernel<D, BF16, CAUSAL, NW, true>), dim3((unsigned)total),
+                     dim3(NW * 64), 0, stream, args);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  constexpr int RPB = 256 / (D / 4);
+  const int64_t merge_blocks = bh * args.split.n_merge * ((BM + RPB - 1) / RPB);
+  if (merge_blocks > 0x7fffffff) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((fa_merge_kernel<D, BF16>), dim3((unsigned)merge_blocks), dim3(256), 0,
+                     stream, args, BM);
   return hipGetLastError();
 }
 
@@ -540,6 +670,81 @@ hipError_t launch_causal(const KernelArgs& a, hipStream_t stream) {
 }
 
 }  // namespace
+
+int block_rows(const KernelArgs& a) {
+  // The choice launch_causal makes.
+  if (a.causal) return (!a.bf16 && a.seq_len >= kWideCausalMinSeq) ? 256 : 128;
+  return a.seq_len >= kWideMinSeq ? 256 : 128;
+}
+
+size_t plan_split(const KernelArgs& a, int compute_units, SplitPlan* plan) {
+  plan->n_items = plan->n_slots = plan->n_merge = 0;
+  constexpr int BN = 64;
+  const int BM = block_rows(a);
+  const int N = a.seq_len;
+  const int nq = (N + BM - 1) / BM;
+  if (compute_units < 1 || nq > kMaxSplitItems) return 0;
+  auto tiles = [&](int qb) {
+    const int kv = a.causal ? std::min(N, (qb + 1) * BM) : N;
+    return (kv + BN - 1) / BN;
+  };
+  // Workgroup slots of the machine: two 4-wave workgroups or one 8-wave
+  // workgroup per CU.  The unsplit grid finishes no earlier than its longest
+  // q-tile (t_max key tiles) and no earlier than the average load per slot;
+  // split only when the longest q-tile clearly dominates.
+  const int64_t slots = (int64_t)compute_units * (BM == 128 ? 2 : 1);
+  int64_t sum = 0;
+  int t_max = 0;
+  for (int qb = 0; qb < nq; ++qb) {
+    sum += tiles(qb);
+    t_max = std::max(t_max, tiles(qb));
+  }
+  const double avg = (double)sum * a.batch * a.heads / (double)slots;
+  if (t_max <= 1.5 * avg + 8.0) return 0;
+  // Chunks of at most S key tiles, S about the average load (at least 8
+  // tiles, so the per-item prologue and the partial write stay small).
+  int64_t S = std::max<int64_t>(8, (int64_t)std::ceil(avg));
+  auto n_chunks = [&](int qb) { return (int)std::min<int64_t>(255, (tiles(qb) + S - 1) / S); };
+  for (;;) {
+    int64_t items = 0;
+    for (int qb = 0; qb < nq; ++qb) items += n_chunks(qb);
+    if (items <= kMaxSplitItems) break;
+    S *= 2;
+  }
+  // Items, longest first (the dispatch order of the grid).
+  struct Item { int len, qb, c, nch; };
+  Item list[kMaxSplitItems];
+  int n = 0, slot_base[kMaxSplitItems], n_slots = 0, n_merge = 0;
+  for (int qb = 0; qb < nq; ++qb) {
+    const int nch = n_chunks(qb), T = tiles(qb);
+    slot_base[qb] = n_slots;
+    if (nch > 1) {
+      plan->merge[n_merge] = (uint32_t)qb | ((uint32_t)nch << 16);
+      plan->merge_slot[n_merge] = (uint16_t)n_slots;
+      ++n_merge;
+      n_slots += nch;
+    }
+    for (int c = 0; c < nch; ++c) {
+      // Same split of [0, T) as the kernel's t_begin / t_end.
+      const int len = (int)((int64_t)(c + 1) * T / nch) - (int)((int64_t)c * T / nch);
+      list[n++] = Item{len, qb, c, nch};
+    }
+  }
+  if (n_merge == 0) return 0;
+  std::stable_sort(list, list + n, [](const Item& x, const Item& y) {
+    return x.len != y.len ? x.len > y.len : x.qb > y.qb;
+  });
+  for (int i = 0; i < n; ++i) {
+    plan->item[i] = (uint32_t)list[i].qb | ((uint32_t)list[i].c << 16) |
+                    ((uint32_t)list[i].nch << 24);
+    plan->slot[i] = (uint16_t)(list[i].nch > 1 ? slot_base[list[i].qb] : 0);
+  }
+  plan->n_items = n;
+  plan->n_slots = n_slots;
+  plan->n_merge = n_merge;
+  // Partial O (fp32) then (m, l) per row of every slot.
+  return (size_t)a.batch * a.heads * n_slots * BM * ((size_t)a.head_dim * 4 + 8);
+}
 
 hipError_t launch_fwd(const KernelArgs& a, hipStream_t stream) {
   if (a.head_dim == 128)

@@ -6,8 +6,10 @@
 // forward(q, k, v, o=None, benchmark=False) -> (o, ms), the same validation
 // messages where the rule is the same, output allocated with empty_like(q)
 // when o is not given, launch on the current stream.  It adds keyword
-// arguments causal, softmax_scale and return_lse, and accepts bf16, head_dim
-// 64, any seq_len >= 1 and strided [B,H,N,D] views with unit head_dim stride.
+// arguments causal, softmax_scale, return_lse and split_kv, and accepts bf16,
+// head_dim 64, any seq_len >= 1 and strided [B,H,N,D] views with unit
+// head_dim stride.  With split_kv the split-KV workspace comes from torch's
+// caching allocator on the current stream.
 //
 // All device work goes through the C ABI in include/fa_mi355x.h; this file
 // holds no kernels and no HIP calls besides fetching the current stream.
@@ -81,7 +83,7 @@ fa_fwd_params make_params(const torch::Tensor& q, const torch::Tensor& k, const 
 std::tuple<torch::Tensor, double, std::optional<torch::Tensor>> fa_forward(
     const torch::Tensor& q, const torch::Tensor& k, const torch::Tensor& v,
     std::optional<torch::Tensor> o_opt, bool benchmark, bool causal,
-    std::optional<double> softmax_scale, bool return_lse) {
+    std::optional<double> softmax_scale, bool return_lse, bool split_kv) {
   validate_inputs(q, k, v, o_opt);
   TORCH_CHECK(q.size(0) <= INT32_MAX && q.size(1) <= INT32_MAX && q.size(2) <= INT32_MAX,
               "shape does not fit 32-bit sizes");
@@ -98,8 +100,23 @@ std::tuple<torch::Tensor, double, std::optional<torch::Tensor>> fa_forward(
   fa_fwd_params p = make_params(q, k, v, o, lse ? lse->data_ptr<float>() : nullptr, causal, scale);
   void* stream = at::hip::getCurrentHIPStreamMasqueradingAsCUDA(q.device().index()).stream();
 
+  uint64_t ws_bytes = 0;
+  if (split_kv) {
+    const fa_status s = fa_fwd_workspace_size(&p, &ws_bytes);
+    TORCH_CHECK(s == FA_OK, "flash attention forward failed: ", fa_status_str(s), ": ",
+                fa_last_error());
+  }
+  torch::Tensor ws;
+  if (ws_bytes > 0) ws = torch::empty({(int64_t)ws_bytes}, q.options().dtype(torch::kUInt8));
+  void* wsp = ws_bytes > 0 ? ws.data_ptr() : nullptr;
+
   float ms = 0.0f;
-  const fa_status s = benchmark ? fa_fwd_timed(&p, stream, &ms) : fa_fwd(&p, stream);
+  fa_status s;
+  if (split_kv)
+    s = benchmark ? fa_fwd_ws_timed(&p, wsp, ws_bytes, stream, &ms)
+                  : fa_fwd_ws(&p, wsp, ws_bytes, stream);
+  else
+    s = benchmark ? fa_fwd_timed(&p, stream, &ms) : fa_fwd(&p, stream);
   TORCH_CHECK(s == FA_OK, "flash attention forward failed: ", fa_status_str(s), ": ",
               fa_last_error());
   return {o, static_cast<double>(ms), lse};
@@ -129,7 +146,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("forward", &fa_forward, pybind11::arg("q"), pybind11::arg("k"), pybind11::arg("v"),
         pybind11::arg("o") = std::optional<torch::Tensor>{}, pybind11::arg("benchmark") = false,
         pybind11::arg("causal") = false, pybind11::arg("softmax_scale") = std::optional<double>{},
-        pybind11::arg("return_lse") = false, "FlashAttention-2 forward (MI355X / gfx950, HIP)");
+        pybind11::arg("return_lse") = false, pybind11::arg("split_kv") = true,
+        "FlashAttention-2 forward (MI355X / gfx950, HIP)");
   m.def("device_info", &device_info, pybind11::arg("device") = 0,
         "hipDeviceProp summary and dense fp16/bf16 MFMA peak");
   m.def("version", []() { return std::string(fa_version()); });

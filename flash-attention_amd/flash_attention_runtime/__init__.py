@@ -5,8 +5,11 @@ Drop-in for the reference package ``flash_attention_runtime``
 returns ``o`` and ``forward_timed(q, k, v, o=None)`` returns ``(o, ms)``, with
 q, k, v laid out [B, H, N, D] on the GPU.  Keyword-only extensions:
 ``causal`` (top-left aligned mask), ``softmax_scale`` (default 1/sqrt(D), as
-the reference) and ``return_lse`` (also return the natural-log logsumexp,
-fp32 [B, H, N]).
+the reference), ``return_lse`` (also return the natural-log logsumexp,
+fp32 [B, H, N]) and ``split_kv`` (default True: problems whose grid would
+leave most CUs idle behind a few long q-tiles split their key ranges across
+workgroups, with an fp32 workspace from torch's allocator; False always runs
+one workgroup per q-tile).
 
 The reference JIT-compiles its CUDA extension on first use
 (``__init__.py:10-27``); here the HIP library ``libfa_mi355x.so`` and the
@@ -49,12 +52,13 @@ def forward(
     causal: bool = False,
     softmax_scale: float | None = None,
     return_lse: bool = False,
+    split_kv: bool = True,
 ):
     """softmax(q k^T * scale [+ causal mask]) v.
 
     Returns ``o`` (same dtype as q), or ``(o, lse)`` when ``return_lse``.
     """
-    out, _ms, lse = _EXT.forward(q, k, v, o, False, causal, softmax_scale, return_lse)
+    out, _ms, lse = _EXT.forward(q, k, v, o, False, causal, softmax_scale, return_lse, split_kv)
     return (out, lse) if return_lse else out
 
 
@@ -67,13 +71,14 @@ def forward_timed(
     causal: bool = False,
     softmax_scale: float | None = None,
     return_lse: bool = False,
+    split_kv: bool = True,
 ):
     """Like ``forward`` but also returns the kernel time in ms measured with
     two HIP events on the current stream (blocks until the kernel ends).
 
     Returns ``(o, ms)``, or ``(o, ms, lse)`` when ``return_lse``.
     """
-    out, ms, lse = _EXT.forward(q, k, v, o, True, causal, softmax_scale, return_lse)
+    out, ms, lse = _EXT.forward(q, k, v, o, True, causal, softmax_scale, return_lse, split_kv)
     return (out, ms, lse) if return_lse else (out, ms)
 
 

@@ -17,6 +17,12 @@
  *   - fa_device_info  <- utils/get_gpu_hardware_param.cu:1-26 and the peak
  *                        table infer_device_peak_specs
  *                        benchmark/cpp/include/perf_metrics.cuh:78-120
+ *   - fa_fwd_ws, fa_fwd_ws_timed, fa_fwd_workspace_size, fa_fwd_plan:
+ *                        no counterpart in the reference (its kernel has one
+ *                        workgroup per q-tile); the workspace variants of
+ *                        fa_fwd / fa_fwd_timed add split-KV for problems
+ *                        whose grid would leave most CUs idle behind a few
+ *                        long q-tiles (short causal sequences, few heads).
  *
  * Semantics (all entry points):
  *   O[b,h,i,:] = sum_j softmax_j(scale * Q[b,h,i,:].K[b,h,j,:] + mask_ij) V[b,h,j,:]
@@ -28,7 +34,8 @@
  * O has the input dtype; LSE is fp32 [batch, heads, seq_len], contiguous,
  * and optional.
  *
- * Ownership: all pointers are borrowed; the library allocates no device memory.
+ * Ownership: all pointers are borrowed; the library allocates no device memory
+ * (the split-KV partials live in a workspace the caller provides).
  * Threading: re-entrant; the only mutable global state is a thread-local error
  * string.  Streams: fa_fwd is asynchronous on `stream`; unlike the reference
  * kernel, an unsupported argument never turns into a silent device no-op —
@@ -96,6 +103,24 @@ typedef struct {
   double hbm_peak_gbps;
 } fa_device_info_t;
 
+/* Split-KV plan of a problem (diagnostic; filled by fa_fwd_plan). */
+#define FA_PLAN_MAX_ITEMS 128
+typedef struct {
+  int32_t block_rows;       /* query rows per workgroup (q-tile height) of the kernel */
+  int32_t n_items;          /* workgroups per (batch, head); 0: the problem runs unsplit */
+  int32_t n_slots;          /* partial-result slots per (batch, head) in the workspace */
+  int32_t n_merge;          /* q-tiles with more than one chunk (merged by a second kernel) */
+  uint64_t workspace_bytes; /* bytes fa_fwd_ws needs (0 when unsplit) */
+  /* Work item i (dispatch order, longest first): q-tile q_tile[i], key tiles
+   * (64 keys each) [tile_begin[i], tile_end[i]) of its n_chunks[i] chunks,
+   * partial slot slot[i] (-1 for a q-tile of one chunk, stored directly). */
+  int32_t q_tile[FA_PLAN_MAX_ITEMS];
+  int32_t tile_begin[FA_PLAN_MAX_ITEMS];
+  int32_t tile_end[FA_PLAN_MAX_ITEMS];
+  int32_t n_chunks[FA_PLAN_MAX_ITEMS];
+  int32_t slot[FA_PLAN_MAX_ITEMS];
+} fa_fwd_plan_t;
+
 /* Host-only argument check; touches no GPU.  Returns FA_OK or the first
  * failing rule (see fa_status).  Replaces _ext.cu:19-57. */
 fa_status fa_fwd_validate(const fa_fwd_params* p);
@@ -108,6 +133,29 @@ fa_status fa_fwd(const fa_fwd_params* p, void* stream);
  * finished and writes its elapsed time in milliseconds to *ms.
  * Replaces the benchmark=true branch of fa_forward (_ext.cu:136-155). */
 fa_status fa_fwd_timed(const fa_fwd_params* p, void* stream, float* ms);
+
+/* Workspace bytes fa_fwd_ws needs for *p on the calling thread's current
+ * device (0: the problem runs unsplit and fa_fwd_ws equals fa_fwd).
+ * Queries the device's CU count; launches nothing. */
+fa_status fa_fwd_workspace_size(const fa_fwd_params* p, uint64_t* bytes);
+
+/* fa_fwd with a device workspace of `workspace_bytes` bytes (16-byte
+ * aligned, contents undefined on entry, overwritten): long key ranges may be
+ * split across workgroups whose fp32 partials go to the workspace and are
+ * merged by a second kernel on `stream`.  The result equals fa_fwd's within
+ * fp32 rounding of the merge (not bit for bit).  FA_ERR_ARG if workspace_bytes
+ * is below fa_fwd_workspace_size; workspace may be NULL only when that size
+ * is 0.  Calls that share a workspace must be ordered (same stream). */
+fa_status fa_fwd_ws(const fa_fwd_params* p, void* workspace, uint64_t workspace_bytes,
+                    void* stream);
+
+/* fa_fwd_ws bracketed by two HIP events on `stream`, as fa_fwd_timed. */
+fa_status fa_fwd_ws_timed(const fa_fwd_params* p, void* workspace, uint64_t workspace_bytes,
+                          void* stream, float* ms);
+
+/* The split plan fa_fwd_ws would use for *p on a device with
+ * `compute_units` CUs.  Host only; touches no GPU. */
+fa_status fa_fwd_plan(const fa_fwd_params* p, int32_t compute_units, fa_fwd_plan_t* out);
 
 /* Static description of a status code. */
 const char* fa_status_str(fa_status s);

@@ -57,6 +57,24 @@ class FaDeviceInfo(ctypes.Structure):
     ]
 
 
+FA_PLAN_MAX_ITEMS = 128
+
+
+class FaFwdPlan(ctypes.Structure):
+    _fields_ = [
+        ("block_rows", ctypes.c_int32),
+        ("n_items", ctypes.c_int32),
+        ("n_slots", ctypes.c_int32),
+        ("n_merge", ctypes.c_int32),
+        ("workspace_bytes", ctypes.c_uint64),
+        ("q_tile", ctypes.c_int32 * FA_PLAN_MAX_ITEMS),
+        ("tile_begin", ctypes.c_int32 * FA_PLAN_MAX_ITEMS),
+        ("tile_end", ctypes.c_int32 * FA_PLAN_MAX_ITEMS),
+        ("n_chunks", ctypes.c_int32 * FA_PLAN_MAX_ITEMS),
+        ("slot", ctypes.c_int32 * FA_PLAN_MAX_ITEMS),
+    ]
+
+
 def declared_functions(header: str = HEADER) -> list[str]:
     """Names of the functions declared in the public header."""
     text = open(header).read()
@@ -72,6 +90,15 @@ def load(path: str = LIB_PATH):
     L.fa_fwd.restype = ctypes.c_int
     L.fa_fwd_timed.argtypes = [P, ctypes.c_void_p, ctypes.POINTER(ctypes.c_float)]
     L.fa_fwd_timed.restype = ctypes.c_int
+    L.fa_fwd_workspace_size.argtypes = [P, ctypes.POINTER(ctypes.c_uint64)]
+    L.fa_fwd_workspace_size.restype = ctypes.c_int
+    L.fa_fwd_ws.argtypes = [P, ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p]
+    L.fa_fwd_ws.restype = ctypes.c_int
+    L.fa_fwd_ws_timed.argtypes = [P, ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p,
+                                  ctypes.POINTER(ctypes.c_float)]
+    L.fa_fwd_ws_timed.restype = ctypes.c_int
+    L.fa_fwd_plan.argtypes = [P, ctypes.c_int32, ctypes.POINTER(FaFwdPlan)]
+    L.fa_fwd_plan.restype = ctypes.c_int
     L.fa_status_str.argtypes = [ctypes.c_int]
     L.fa_status_str.restype = ctypes.c_char_p
     L.fa_last_error.argtypes = []

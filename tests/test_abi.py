@@ -64,7 +64,8 @@ def check(lib, p, expect, msg=None):
 def test_every_declared_function_is_exported(lib):
     names = A.declared_functions()
     assert set(names) >= {"fa_fwd", "fa_fwd_validate", "fa_fwd_timed", "fa_status_str",
-                          "fa_last_error", "fa_device_info", "fa_version"}
+                          "fa_last_error", "fa_device_info", "fa_version", "fa_fwd_ws",
+                          "fa_fwd_ws_timed", "fa_fwd_workspace_size", "fa_fwd_plan"}
     for n in names:
         assert hasattr(lib, n), f"{n} declared in include/fa_mi355x.h but not exported"
 
@@ -107,8 +108,13 @@ int main(void) {
   F(fa_device_info_t, l2_bytes); F(fa_device_info_t, memory_bus_width_bits);
   F(fa_device_info_t, memory_clock_khz); F(fa_device_info_t, fp16_dense_peak_tflops);
   F(fa_device_info_t, hbm_peak_gbps);
-  printf("\"sizeof.fa_fwd_params\": [%zu, 0], \"sizeof.fa_device_info_t\": [%zu, 0]}\n",
-         sizeof(fa_fwd_params), sizeof(fa_device_info_t));
+  F(fa_fwd_plan_t, block_rows); F(fa_fwd_plan_t, n_items); F(fa_fwd_plan_t, n_slots);
+  F(fa_fwd_plan_t, n_merge); F(fa_fwd_plan_t, workspace_bytes); F(fa_fwd_plan_t, q_tile);
+  F(fa_fwd_plan_t, tile_begin); F(fa_fwd_plan_t, tile_end); F(fa_fwd_plan_t, n_chunks);
+  F(fa_fwd_plan_t, slot);
+  printf("\"sizeof.fa_fwd_params\": [%zu, 0], \"sizeof.fa_device_info_t\": [%zu, 0], "
+         "\"sizeof.fa_fwd_plan_t\": [%zu, 0]}\n",
+         sizeof(fa_fwd_params), sizeof(fa_device_info_t), sizeof(fa_fwd_plan_t));
   return 0;
 }
 """
@@ -123,7 +129,8 @@ def test_ctypes_struct_layout_matches_c(tmp_path):
     subprocess.run(["gcc", "-std=c99", "-I", os.path.dirname(A.HEADER), str(src), "-o", str(exe)],
                    check=True)
     c = json.loads(subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout)
-    for cls, cname in ((A.FaFwdParams, "fa_fwd_params"), (A.FaDeviceInfo, "fa_device_info_t")):
+    for cls, cname in ((A.FaFwdParams, "fa_fwd_params"), (A.FaDeviceInfo, "fa_device_info_t"),
+                       (A.FaFwdPlan, "fa_fwd_plan_t")):
         for fname, _ in cls._fields_:
             off, size = c[f"{cname}.{fname}"]
             desc = getattr(cls, fname)
@@ -301,6 +308,23 @@ def test_fwd_timed_rejects_before_launch(lib):
     p.softmax_scale = -1.0
     assert lib.fa_fwd_timed(ctypes.byref(p), None, ctypes.byref(ms)) == A.FA_ERR_ARG
     assert ms.value == 0.0  # *ms is reset on every call that gets that far
+
+
+def test_fwd_ws_rejects_before_launch(lib):
+    p = contiguous(D=96)
+    p.head_dim = 96
+    assert lib.fa_fwd_ws(ctypes.byref(p), None, 0, None) == A.FA_ERR_HEADDIM
+    # a size without a buffer is rejected before anything else
+    assert lib.fa_fwd_ws(ctypes.byref(contiguous()), None, 4096, None) == A.FA_ERR_NULL
+    assert "workspace is NULL" in lib.fa_last_error().decode()
+    ms = ctypes.c_float(-1.0)
+    assert lib.fa_fwd_ws_timed(ctypes.byref(contiguous()), None, 16, None,
+                               ctypes.byref(ms)) == A.FA_ERR_NULL
+    assert ms.value == 0.0
+    size = ctypes.c_uint64(7)
+    assert lib.fa_fwd_workspace_size(ctypes.byref(p), ctypes.byref(size)) == A.FA_ERR_HEADDIM
+    assert size.value == 0
+    assert lib.fa_fwd_workspace_size(ctypes.byref(contiguous()), None) == A.FA_ERR_NULL
 
 
 def test_device_info_null(lib):

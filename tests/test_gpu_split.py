@@ -1,0 +1,304 @@
+"""GPU parity of split-KV (fa_fwd_ws): long key ranges of a q-tile computed
+by several workgroups whose fp32 partials are merged by a second kernel.
+
+Every case first asks the library (fa_fwd_plan with this device's CU count)
+for its plan and asserts that it really splits, so these tests cannot pass
+on the unsplit path by accident.  The split result is checked against the
+fp64 oracle and the reference-kernel emulator (same bars as the unsplit
+kernel), against the unsplit result of the same inputs, and for the merge's
+own edge cases: chunks whose rows see no key, score jumps between chunks,
+ragged tails, strided outputs inside a larger buffer, LSE, graph capture.
+Direct C-ABI calls (ctypes, raw device pointers) cover the workspace
+contract: size query, rejection of a short or misaligned workspace with the
+output untouched, and the timed variant.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import abi_ctypes as A
+from helpers import LSE_TOL, MAX_ABS_TOL, case_seed, err_stats, make_config, make_qkv, to_np32
+from test_gpu_parity import _check_against_oracle, _sample_rows, _scale_keys
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def _note(msg):
+    print(msg, flush=True)
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return A.load()
+
+
+@pytest.fixture(scope="module")
+def cus(fa):
+    return int(fa.device_info(0)["compute_units"])
+
+
+def _plan(lib, cus, q, k, v, o, causal):
+    p = A.params_from_tensors(q, k, v, o, None, causal)
+    pl = A.FaFwdPlan()
+    assert lib.fa_fwd_plan(ctypes.byref(p), cus, ctypes.byref(pl)) == A.FA_OK
+    return pl
+
+
+def _assert_split(lib, cus, q, k, v, causal):
+    pl = _plan(lib, cus, q, k, v, torch.empty_like(q), causal)
+    _note(f"  plan: BM={pl.block_rows} items={pl.n_items} slots={pl.n_slots} "
+          f"merge={pl.n_merge} workspace={pl.workspace_bytes}")
+    assert pl.n_items > 0 and pl.n_merge > 0, "expected a split plan on this device"
+    return pl
+
+
+def _both(fa, q, k, v, causal, scale=None):
+    o, lse = fa.forward(q, k, v, causal=causal, softmax_scale=scale, return_lse=True)
+    o1, lse1 = fa.forward(q, k, v, causal=causal, softmax_scale=scale, return_lse=True,
+                          split_kv=False)
+    torch.cuda.synchronize()
+    return o, lse, o1, lse1
+
+
+def _vs_unsplit(o, lse, o1, lse1, dtype):
+    """Split and unsplit differ where the exponent offsets sit (each chunk
+    has its own), so P rounds differently before P.V (2^-11 relative for
+    fp16, 2^-8 for bf16, per term), and by the fp32 merge.  A merge mistake
+    (a wrong weight, slot or row) shows as an error of the order of |O|.
+    LSE: fp16 sums the rounded P (relative error <= 2^-11 per term, so each
+    of ln l_split and ln l_unsplit is within 2^-11 of the exact value); bf16
+    sums the unrounded fp32 p on both paths."""
+    d = (o.float() - o1.float()).abs()
+    u = 2.0 ** -9 if dtype == "fp16" else 2.0 ** -6
+    n_bad = int((d > u * (1.0 + o1.float().abs())).sum().item())
+    dl = (lse - lse1).abs().max().item()
+    _note(f"  vs unsplit: max|dO|={d.max().item():.3e} mean|dO|={d.mean().item():.3e} "
+          f"over-bound={n_bad} max|dLSE|={dl:.3e}")
+    assert n_bad == 0
+    assert d.mean().item() <= u / 8
+    assert dl <= (2.0 ** -10 + 1e-5 if dtype == "fp16" else 1e-4)
+
+
+@pytest.mark.parametrize("causal", [False, True], ids=["noncausal", "causal"])
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("N", [700, 1024, 1537])
+def test_split_small_vs_oracle(fa, oracle, lib, cus, N, D, dtype, causal):
+    """One or two heads: the unsplit grid would occupy a few CUs, so every
+    q-tile beyond 8 key tiles is split.  Ragged N included."""
+    H = 2 if N < 1500 else 1
+    _note(f"case split small N={N} D={D} {dtype} causal={causal}")
+    q, k, v = make_qkv(1, H, N, D, dtype, seed=case_seed(900 + N + D), device=DEV)
+    _assert_split(lib, cus, q, k, v, causal)
+    o, lse, o1, lse1 = _both(fa, q, k, v, causal)
+    _check_against_oracle(oracle, q, k, v, o, lse, causal, 1.0 / math.sqrt(D), dtype)
+    _vs_unsplit(o, lse, o1, lse1, dtype)
+
+
+@pytest.mark.parametrize("pattern", ["jump", "ramp", "half", "drop"])
+@pytest.mark.parametrize("causal", [False, True], ids=["noncausal", "causal"])
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+def test_split_score_jumps_vs_oracle(fa, oracle, lib, cus, pattern, causal, dtype):
+    """Scores that jump between key tiles put the chunks' offsets m_c far
+    apart ("drop": the first chunk holds the max, later chunks' weights
+    underflow toward 0; "ramp": the last chunk dominates)."""
+    _note(f"case split jumps pattern={pattern} {dtype} causal={causal}")
+    N, D = 1280, 128
+    q, k, v = make_qkv(1, 1, N, D, dtype, seed=case_seed(901), device="cpu")
+    tdt = torch.float16 if dtype == "fp16" else torch.bfloat16
+    k = _scale_keys(k, pattern).to(tdt)
+    q, k, v = q.to(DEV), k.to(DEV), v.to(DEV)
+    _assert_split(lib, cus, q, k, v, causal)
+    o, lse, o1, lse1 = _both(fa, q, k, v, causal)
+    _check_against_oracle(oracle, q, k, v, o, lse, causal, 1.0 / math.sqrt(D), dtype,
+                          contract=False)
+
+
+@pytest.mark.parametrize("scale", [0.01, 3.0])
+def test_split_softmax_scale_vs_oracle(fa, oracle, lib, cus, scale):
+    """Flat (scale 0.01) and peaked (scale 3) rows through the merge."""
+    _note(f"case split scale={scale}")
+    N, D = 1024, 64
+    q, k, v = make_qkv(1, 2, N, D, "fp16", seed=case_seed(902), device=DEV)
+    _assert_split(lib, cus, q, k, v, True)
+    o, lse, o1, lse1 = _both(fa, q, k, v, True, scale)
+    _check_against_oracle(oracle, q, k, v, o, lse, True, scale, "fp16", contract=False)
+
+
+def test_split_c5r_matches_unsplit_and_is_split(fa, lib, cus):
+    """C5r (B1 H16 N3000 causal fp16): the BASELINE configuration the split
+    exists for.  Its sampled rows are checked against the oracle by
+    test_config_sampled_rows_vs_oracle (which runs the default, split path);
+    here: the plan splits, and split == unsplit within two roundings."""
+    _note("case split C5r")
+    q, k, v, causal, scale = make_config("C5r", device=DEV)
+    pl = _assert_split(lib, cus, q, k, v, causal)
+    assert pl.block_rows == 128
+    o, lse, o1, lse1 = _both(fa, q, k, v, causal)
+    assert torch.isfinite(o).all().item()
+    _vs_unsplit(o, lse, o1, lse1, "fp16")
+
+
+@pytest.mark.parametrize("causal,N,H", [(True, 8192, 2), (False, 4096, 1)],
+                         ids=["causal8192", "noncausal4096"])
+def test_split_wide_workgroup_sampled_rows(fa, oracle, lib, cus, causal, N, H):
+    """8-wave workgroups (BM = 256) with the optimistic pass, split: sampled
+    rows against the oracle and the reference-kernel emulator."""
+    _note(f"case split wide causal={causal} N={N} H={H}")
+    D = 128
+    q, k, v = make_qkv(1, H, N, D, "fp16", seed=case_seed(903), device=DEV)
+    pl = _assert_split(lib, cus, q, k, v, causal)
+    assert pl.block_rows == 256
+    o, lse, o1, lse1 = _both(fa, q, k, v, causal)
+    _vs_unsplit(o, lse, o1, lse1, "fp16")
+    rng = np.random.default_rng(903)
+    heads, sel_bh, sel_row = _sample_rows(N, H, rng, n_random=32)
+    qn, kn, vn = to_np32(q), to_np32(k), to_np32(v)
+    scale = 1.0 / math.sqrt(D)
+    ref_o, ref_lse = oracle.attn_rows_f64(qn, kn, vn, scale, causal, sel_bh, sel_row)
+    emu_o, _ = oracle.kernel_numerics_rows(qn, kn, vn, scale, causal, sel_bh, sel_row, oracle.F16)
+    got_o = to_np32(o.reshape(H, N, D))[sel_bh, sel_row]
+    got_lse = to_np32(lse.reshape(H, N))[sel_bh, sel_row]
+    mx, mean = err_stats(got_o, ref_o)
+    emx, emean = err_stats(emu_o, ref_o)
+    lse_err = float(np.abs(got_lse.astype(np.float64) - ref_lse).max())
+    _note(f"  sampled {len(sel_row)} rows: max_abs={mx:.3e} mean_abs={mean:.3e} "
+          f"(ref-kernel emu {emx:.3e}/{emean:.3e}) lse={lse_err:.3e}")
+    assert mx <= MAX_ABS_TOL
+    assert mx <= 2 * emx + 1e-6 and mean <= 2 * emean + 1e-6
+    assert lse_err <= LSE_TOL
+
+
+def test_split_strided_output_in_padded_buffer(fa, oracle, lib, cus):
+    """BNHD views with a padded seq stride for Q, K, V and O; O lives inside a
+    NaN-filled buffer: the split kernel and the merge write exactly the view."""
+    _note("case split strided")
+    B, H, N, D = 1, 2, 1000, 64
+    q, k, v = make_qkv(B, H, N, D, "bf16", seed=case_seed(904), device=DEV)
+
+    def bnhd(t, pad):
+        buf = torch.full((B, N, H, D + pad), float("nan"), dtype=t.dtype, device=DEV)
+        view = buf[..., :D].permute(0, 2, 1, 3)
+        view.copy_(t)
+        return buf, view
+
+    _, qv = bnhd(q, 8)
+    _, kv = bnhd(k, 16)
+    _, vv = bnhd(v, 0)
+    obuf, ov = bnhd(torch.zeros_like(q), 24)
+    obuf.fill_(float("nan"))
+    _assert_split(lib, cus, qv, kv, vv, True)
+    out, lse = fa.forward(qv, kv, vv, ov, causal=True, return_lse=True)
+    torch.cuda.synchronize()
+    assert out.data_ptr() == ov.data_ptr()
+    assert torch.isnan(obuf[..., D:]).all().item(), "padding of O was written"
+    _check_against_oracle(oracle, q, k, v, ov, lse, True, 1.0 / math.sqrt(D), "bf16")
+
+
+def test_split_deterministic_and_graph_replay(fa, lib, cus):
+    """Split results are deterministic (no atomics), and a captured graph
+    (workspace from the graph's pool) replays to the eager result, several
+    times, with eager work in between."""
+    _note("case split graph")
+    q, k, v = make_qkv(1, 4, 2000, 128, "fp16", seed=case_seed(905), device=DEV)
+    _assert_split(lib, cus, q, k, v, True)
+    ref = fa.forward(q, k, v, causal=True)
+    again = fa.forward(q, k, v, causal=True)
+    torch.cuda.synchronize()
+    assert torch.equal(ref, again)
+    o = torch.empty_like(q)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fa.forward(q, k, v, o, causal=True)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fa.forward(q, k, v, o, causal=True)
+    for rep in range(3):
+        o.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(o, ref), f"replay {rep}"
+        e = fa.forward(q, k, v, causal=True, split_kv=False)
+        torch.cuda.synchronize()
+        assert torch.isfinite(e).all().item()
+
+
+# ------------------------------------------------------------ the C ABI directly
+
+
+def _stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def test_abi_workspace_contract(fa, lib, cus):
+    """fa_fwd_workspace_size, fa_fwd_ws and fa_fwd_ws_timed through ctypes."""
+    _note("case split abi")
+    q, k, v = make_qkv(1, 2, 1024, 128, "fp16", seed=case_seed(906), device=DEV)
+    o = torch.full_like(q, float("nan"))
+    lse = torch.empty((1, 2, 1024), dtype=torch.float32, device=DEV)
+    p = A.params_from_tensors(q, k, v, o, lse, True)
+    need = ctypes.c_uint64(0)
+    assert lib.fa_fwd_workspace_size(ctypes.byref(p), ctypes.byref(need)) == A.FA_OK
+    pl = _plan(lib, cus, q, k, v, o, True)
+    assert need.value == pl.workspace_bytes > 0
+    ws = torch.empty(need.value + 256, dtype=torch.uint8, device=DEV)
+    torch.cuda.synchronize()
+
+    # rejected before any launch: O keeps its NaN fill
+    assert lib.fa_fwd_ws(ctypes.byref(p), None, 0, _stream()) == A.FA_ERR_NULL
+    assert lib.fa_fwd_ws(ctypes.byref(p), ctypes.c_void_p(ws.data_ptr()), need.value - 1,
+                         _stream()) == A.FA_ERR_ARG
+    assert "smaller than" in lib.fa_last_error().decode()
+    assert lib.fa_fwd_ws(ctypes.byref(p), ctypes.c_void_p(ws.data_ptr() + 8), need.value,
+                         _stream()) == A.FA_ERR_STRIDE
+    torch.cuda.synchronize()
+    assert torch.isnan(o).all().item()
+
+    # exact size, through fa_fwd_ws, equals the torch path (same plan)
+    assert lib.fa_fwd_ws(ctypes.byref(p), ctypes.c_void_p(ws.data_ptr()), need.value,
+                         _stream()) == A.FA_OK
+    torch.cuda.synchronize()
+    ref, ref_lse = fa.forward(q, k, v, causal=True, return_lse=True)
+    torch.cuda.synchronize()
+    assert torch.equal(o, ref) and torch.equal(lse, ref_lse)
+
+    # LSE optional; timed variant
+    o.fill_(float("nan"))
+    p2 = A.params_from_tensors(q, k, v, o, None, True)
+    ms = ctypes.c_float(0.0)
+    assert lib.fa_fwd_ws_timed(ctypes.byref(p2), ctypes.c_void_p(ws.data_ptr()), need.value,
+                               _stream(), ctypes.byref(ms)) == A.FA_OK
+    torch.cuda.synchronize()
+    assert ms.value > 0.0
+    assert torch.equal(o, ref)
+
+    # the plain entry point ignores the split and still matches the unsplit torch path
+    o.fill_(float("nan"))
+    assert lib.fa_fwd(ctypes.byref(p2), _stream()) == A.FA_OK
+    torch.cuda.synchronize()
+    assert torch.equal(o, fa.forward(q, k, v, causal=True, split_kv=False))
+
+
+def test_abi_unsplit_problem_needs_no_workspace(fa, lib):
+    """C3-sized problems need no workspace: fa_fwd_ws(NULL, 0) is fa_fwd."""
+    _note("case split abi unsplit")
+    name = "C2"
+    q, k, v, causal, _ = make_config(name, device=DEV)
+    o = torch.empty_like(q)
+    p = A.params_from_tensors(q, k, v, o, None, causal)
+    need = ctypes.c_uint64(1)
+    assert lib.fa_fwd_workspace_size(ctypes.byref(p), ctypes.byref(need)) == A.FA_OK
+    assert need.value == 0
+    assert lib.fa_fwd_ws(ctypes.byref(p), None, 0, _stream()) == A.FA_OK
+    torch.cuda.synchronize()
+    assert torch.equal(o, fa.forward(q, k, v, causal=causal))

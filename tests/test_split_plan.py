@@ -1,0 +1,183 @@
+"""CPU tests of the split-KV work plan (fa_fwd_plan in include/fa_mi355x.h).
+
+The plan decides, on the host, whether a problem's key ranges are split
+across workgroups and how.  The kernel trusts it completely: every key tile
+of every q-tile must be computed by exactly one work item, every split q-tile
+needs its own run of partial slots, and the workspace must hold them all.
+These are the invariants checked here, over the BASELINE configurations and
+a sweep of shapes, for the MI355X's 256 CUs and other CU counts.  Nothing
+here touches a GPU.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import pytest
+
+import abi_ctypes as A
+from test_abi import contiguous
+
+BN = 64  # keys per tile
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return A.load()
+
+
+def plan(lib, p, cus=256):
+    out = A.FaFwdPlan()
+    rc = lib.fa_fwd_plan(ctypes.byref(p), cus, ctypes.byref(out))
+    assert rc == A.FA_OK, lib.fa_last_error().decode()
+    return out
+
+
+def tiles(qb, N, BM, causal):
+    kv = min(N, (qb + 1) * BM) if causal else N
+    return (kv + BN - 1) // BN
+
+
+def check_plan(pl, B, H, N, D, causal):
+    BM = pl.block_rows
+    nq = (N + BM - 1) // BM
+    n = pl.n_items
+    assert 0 < n <= A.FA_PLAN_MAX_ITEMS
+    items = [(pl.q_tile[i], pl.tile_begin[i], pl.tile_end[i], pl.n_chunks[i], pl.slot[i])
+             for i in range(n)]
+    # every key tile of every q-tile exactly once, chunks non-empty
+    by_q = {}
+    for qb, tb, te, nch, slot in items:
+        assert 0 <= qb < nq
+        assert 0 <= tb < te <= tiles(qb, N, BM, causal)
+        by_q.setdefault(qb, []).append((tb, te, nch, slot))
+    assert sorted(by_q) == list(range(nq))
+    slots_used = []
+    merged = 0
+    for qb, chunks in by_q.items():
+        chunks.sort()
+        nch = chunks[0][2]
+        assert all(c[2] == nch for c in chunks) and len(chunks) == nch <= 255
+        assert chunks[0][0] == 0 and chunks[-1][1] == tiles(qb, N, BM, causal)
+        for a, b in zip(chunks, chunks[1:]):
+            assert a[1] == b[0]
+        if nch == 1:
+            assert chunks[0][3] == -1
+        else:
+            merged += 1
+            s = [c[3] for c in chunks]
+            assert s == list(range(s[0], s[0] + nch))  # a run of consecutive slots
+            slots_used += s
+    assert merged == pl.n_merge > 0
+    assert sorted(slots_used) == list(range(pl.n_slots))  # disjoint, dense
+    # dispatch order: longest first
+    lens = [te - tb for _, tb, te, _, _ in items]
+    assert lens == sorted(lens, reverse=True)
+    assert pl.workspace_bytes == B * H * pl.n_slots * BM * (D * 4 + 8)
+    # the split shortens the longest work item
+    assert max(lens) < max(tiles(qb, N, BM, causal) for qb in range(nq))
+
+
+@pytest.mark.parametrize("name,B,H,N,D,causal,dtype,split", [
+    ("C1", 1, 1, 128, 128, 0, A.FA_DTYPE_F16, False),
+    ("C2", 4, 16, 1024, 64, 0, A.FA_DTYPE_F16, False),
+    ("C3", 4, 32, 4096, 128, 0, A.FA_DTYPE_F16, False),
+    ("C4", 2, 32, 8192, 128, 1, A.FA_DTYPE_BF16, False),
+    ("C5", 1, 16, 16384, 128, 1, A.FA_DTYPE_F16, False),
+    ("C5r", 1, 16, 3000, 128, 1, A.FA_DTYPE_F16, True),
+])
+def test_baseline_configs(lib, name, B, H, N, D, causal, dtype, split):
+    """The full-machine configurations run unsplit (nothing to gain); the
+    short causal C5r splits its long q-tiles."""
+    p = contiguous(B=B, H=H, N=N, D=D, dtype=dtype, causal=causal)
+    pl = plan(lib, p)
+    assert pl.block_rows == (256 if (N >= 2048 and not causal) or
+                             (causal and dtype == A.FA_DTYPE_F16 and N >= 8192) else 128)
+    if not split:
+        assert pl.n_items == 0 and pl.workspace_bytes == 0 and pl.n_slots == 0
+    else:
+        check_plan(pl, B, H, N, D, causal)
+
+
+def test_c5r_plan_shape(lib):
+    """C5r on 256 CUs: 24 q-tiles of 2..47 key tiles; average load per
+    workgroup slot 16*599/512 = 18.7 tiles, so chunks of at most 19 tiles:
+    q-tiles of 20..38 tiles in 2 chunks, 40..47 in 3."""
+    pl = plan(lib, contiguous(B=1, H=16, N=3000, D=128, causal=1))
+    check_plan(pl, 1, 16, 3000, 128, 1)
+    assert pl.block_rows == 128
+    assert pl.n_merge == 15 and pl.n_slots == 10 * 2 + 5 * 3
+    assert pl.n_items == 9 + 20 + 15
+    assert max(pl.tile_end[i] - pl.tile_begin[i] for i in range(pl.n_items)) == 19
+
+
+@pytest.mark.parametrize("B,H,N,D,causal,dtype", [
+    (1, 16, 2048, 128, 1, A.FA_DTYPE_F16),
+    (1, 8, 4096, 128, 1, A.FA_DTYPE_BF16),
+    (1, 4, 8192, 128, 1, A.FA_DTYPE_F16),    # 8-wave causal
+    (1, 1, 16384, 64, 1, A.FA_DTYPE_F16),
+    (1, 2, 4096, 128, 0, A.FA_DTYPE_F16),    # few heads, non-causal
+    (1, 1, 16384, 128, 0, A.FA_DTYPE_BF16),  # many chunks per q-tile
+    (2, 3, 3001, 64, 1, A.FA_DTYPE_BF16),    # ragged
+    (1, 1, 32768, 128, 1, A.FA_DTYPE_F16),   # q-tiles beyond the item budget
+])
+def test_split_plans_are_complete(lib, B, H, N, D, causal, dtype):
+    pl = plan(lib, contiguous(B=B, H=H, N=N, D=D, dtype=dtype, causal=causal))
+    BM = pl.block_rows
+    if (N + BM - 1) // BM >= A.FA_PLAN_MAX_ITEMS:
+        assert pl.n_items == 0  # no item left for a second chunk: never split
+        return
+    check_plan(pl, B, H, N, D, causal)
+
+
+@pytest.mark.parametrize("N", [1, 64, 127, 128, 129, 1000, 2047, 2048, 4095, 6000, 8191, 8192,
+                               12000, 16384])
+@pytest.mark.parametrize("causal", [0, 1])
+@pytest.mark.parametrize("H", [1, 3, 16, 64])
+def test_plan_sweep(lib, N, causal, H):
+    """Whatever the shape, a plan is either empty or complete."""
+    for D in (64, 128):
+        for dtype in (A.FA_DTYPE_F16, A.FA_DTYPE_BF16):
+            pl = plan(lib, contiguous(B=1, H=H, N=N, D=D, dtype=dtype, causal=causal))
+            if pl.n_items:
+                check_plan(pl, 1, H, N, D, causal)
+            else:
+                assert pl.workspace_bytes == 0 and pl.n_merge == 0 and pl.n_slots == 0
+
+
+def test_more_cus_split_more(lib):
+    """The split is a response to idle CUs: a machine with fewer CUs runs the
+    same problem unsplit, a larger one splits it."""
+    p = contiguous(B=1, H=16, N=3000, D=128, causal=1)
+    assert plan(lib, p, cus=8).n_items == 0
+    assert plan(lib, p, cus=256).n_items > 0
+    big = plan(lib, p, cus=1024)
+    check_plan(big, 1, 16, 3000, 128, 1)
+    assert big.n_slots >= plan(lib, p, cus=256).n_slots
+
+
+def test_plan_ignores_pointers_and_lse(lib):
+    p1 = contiguous(B=1, H=16, N=3000, D=128, causal=1)
+    p2 = contiguous(B=1, H=16, N=3000, D=128, causal=1, lse=False)
+    p2.q = 0x7000000
+    a, b = plan(lib, p1), plan(lib, p2)
+    assert bytes(a) == bytes(b)
+
+
+def test_plan_rejects(lib):
+    out = A.FaFwdPlan()
+    p = contiguous()
+    assert lib.fa_fwd_plan(ctypes.byref(p), 256, None) == A.FA_ERR_NULL
+    assert lib.fa_fwd_plan(ctypes.byref(p), 0, ctypes.byref(out)) == A.FA_ERR_ARG
+    assert "compute_units" in lib.fa_last_error().decode()
+    p.head_dim = 96
+    assert lib.fa_fwd_plan(ctypes.byref(p), 256, ctypes.byref(out)) == A.FA_ERR_HEADDIM
+    assert out.n_items == 0 and out.workspace_bytes == 0
+
+
+def test_workspace_bound(lib):
+    """Workspace per (batch, head) is at most kMaxSplitItems slots of BM rows:
+    the plan never asks for more than B*H*128*256*(128*4+8) bytes."""
+    for N in (2048, 3000, 4096, 8192, 16384):
+        pl = plan(lib, contiguous(B=1, H=1, N=N, D=128, causal=0))
+        assert pl.workspace_bytes <= 128 * 256 * (128 * 4 + 8)
+        assert pl.n_slots <= A.FA_PLAN_MAX_ITEMS
