@@ -12,6 +12,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdarg>
 #include <cstdint>
@@ -100,13 +101,26 @@ void to_kernel_args(const fa_fwd_params* p, fa::KernelArgs* a) {
   a->split.n_merge = 0;
 }
 
-// Compute units of the calling thread's current device.
+// Compute units of the calling thread's current device (queried once per
+// device; the split plan depends on it).
+constexpr int kMaxDevices = 64;
+std::atomic<int> g_device_cus[kMaxDevices];
+
 fa_status current_compute_units(int* cus) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
-  if (e == hipSuccess) e = hipDeviceGetAttribute(cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e != hipSuccess) return fail(FA_ERR_HIP, "hipGetDevice failed: %s", hipGetErrorString(e));
+  if (dev >= 0 && dev < kMaxDevices) {
+    const int cached = g_device_cus[dev].load(std::memory_order_relaxed);
+    if (cached > 0) {
+      *cus = cached;
+      return FA_OK;
+    }
+  }
+  e = hipDeviceGetAttribute(cus, hipDeviceAttributeMultiprocessorCount, dev);
   if (e != hipSuccess)
     return fail(FA_ERR_HIP, "device query failed: %s", hipGetErrorString(e));
+  if (dev >= 0 && dev < kMaxDevices) g_device_cus[dev].store(*cus, std::memory_order_relaxed);
   return FA_OK;
 }
 

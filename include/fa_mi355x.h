@@ -37,7 +37,8 @@
  * Ownership: all pointers are borrowed; the library allocates no device memory
  * (the split-KV partials live in a workspace the caller provides).
  * Threading: re-entrant; the only mutable global state is a thread-local error
- * string.  Streams: fa_fwd is asynchronous on `stream`; unlike the reference
+ * string and a per-device cache of the CU count (written once, atomically).
+ * Streams: fa_fwd is asynchronous on `stream`; unlike the reference
  * kernel, an unsupported argument never turns into a silent device no-op —
  * it is rejected on the host with a status code before anything is launched.
  */
