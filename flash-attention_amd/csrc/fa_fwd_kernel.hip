@@ -718,8 +718,15 @@ size_t plan_split(const KernelArgs& a, int compute_units, SplitPlan* plan) {
   };
   // Workgroup slots of the machine: two 4-wave workgroups or one 8-wave
   // workgroup per CU.  The unsplit grid finishes no earlier than its longest
-  // q-tile (t_max key tiles) and no earlier than the average load per slot;
-  // split only when the longest q-tile clearly dominates.
+  // q-tile (t_max key tiles) and no earlier than the total load over the
+  // machine's throughput.  A CU running one 4-wave workgroup alone already
+  // reaches ~90 % of its two-workgroup throughput (measured: 1.14 us per
+  // 128x64 tile alone, 2.1 us each for two), so the throughput bound counts
+  // 1.1 workgroups per CU for 4-wave kernels.  Split only when the longest
+  // q-tile clearly dominates that bound: the partials cost an fp32 write
+  // and read of O per chunk, which ate the whole gain at B1 H16 N3000
+  // causal (bound ratio 1.4) and left +11 % at H8 (2.8) and +50 % at
+  // B1 H4 N8192 causal (3.9).
   const int64_t slots = (int64_t)compute_units * (BM == 128 ? 2 : 1);
   int64_t sum = 0;
   int t_max = 0;
@@ -727,8 +734,10 @@ size_t plan_split(const KernelArgs& a, int compute_units, SplitPlan* plan) {
     sum += tiles(qb);
     t_max = std::max(t_max, tiles(qb));
   }
-  const double avg = (double)sum * a.batch * a.heads / (double)slots;
-  if (t_max <= 1.5 * avg + 8.0) return 0;
+  const double total = (double)sum * a.batch * a.heads;
+  const double bound = total / ((double)compute_units * (BM == 128 ? 1.1 : 1.0));
+  if (t_max <= 1.5 * bound + 8.0) return 0;
+  const double avg = total / (double)slots;  // per workgroup slot
   // Chunks of at most S key tiles, S about the average load (at least 8
   // tiles, so the per-item prologue and the partial write stay small).
   int64_t S = std::max<int64_t>(8, (int64_t)std::ceil(avg));

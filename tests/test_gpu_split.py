@@ -132,18 +132,35 @@ def test_split_softmax_scale_vs_oracle(fa, oracle, lib, cus, scale):
     _check_against_oracle(oracle, q, k, v, o, lse, True, scale, "fp16", contract=False)
 
 
-def test_split_c5r_matches_unsplit_and_is_split(fa, lib, cus):
-    """C5r (B1 H16 N3000 causal fp16): the BASELINE configuration the split
-    exists for.  Its sampled rows are checked against the oracle by
-    test_config_sampled_rows_vs_oracle (which runs the default, split path);
-    here: the plan splits, and split == unsplit within two roundings."""
-    _note("case split C5r")
-    q, k, v, causal, scale = make_config("C5r", device=DEV)
-    pl = _assert_split(lib, cus, q, k, v, causal)
+def test_split_c5r_half_heads_vs_oracle_and_unsplit(fa, oracle, lib, cus):
+    """C5r's shape and inputs (N3000 causal fp16, Q, K ~ N(0, 3^2)) with 8 of
+    its 16 heads, which the plan splits into up to 5 chunks per q-tile:
+    sampled rows against the oracle and the reference-kernel emulator, and
+    split == unsplit within two roundings."""
+    _note("case split C5r/2")
+    B, H, N, D = 1, 8, 3000, 128
+    q, k, v = make_qkv(B, H, N, D, "fp16", seed=case_seed(5), qk_sigma=3.0, device=DEV)
+    pl = _assert_split(lib, cus, q, k, v, True)
     assert pl.block_rows == 128
-    o, lse, o1, lse1 = _both(fa, q, k, v, causal)
+    o, lse, o1, lse1 = _both(fa, q, k, v, True)
     assert torch.isfinite(o).all().item()
     _vs_unsplit(o, lse, o1, lse1, "fp16")
+    rng = np.random.default_rng(5)
+    heads, sel_bh, sel_row = _sample_rows(N, H, rng, n_random=48)
+    qn, kn, vn = to_np32(q), to_np32(k), to_np32(v)
+    scale = 1.0 / math.sqrt(D)
+    ref_o, ref_lse = oracle.attn_rows_f64(qn, kn, vn, scale, True, sel_bh, sel_row)
+    emu_o, _ = oracle.kernel_numerics_rows(qn, kn, vn, scale, True, sel_bh, sel_row, oracle.F16)
+    got_o = to_np32(o.reshape(H, N, D))[sel_bh, sel_row]
+    got_lse = to_np32(lse.reshape(H, N))[sel_bh, sel_row]
+    mx, mean = err_stats(got_o, ref_o)
+    emx, emean = err_stats(emu_o, ref_o)
+    lse_err = float(np.abs(got_lse.astype(np.float64) - ref_lse).max())
+    _note(f"  sampled {len(sel_row)} rows: max_abs={mx:.3e} mean_abs={mean:.3e} "
+          f"(ref-kernel emu {emx:.3e}/{emean:.3e}) lse={lse_err:.3e}")
+    assert mx <= MAX_ABS_TOL
+    assert mx <= 2 * emx + 1e-6 and mean <= 2 * emean + 1e-6
+    assert lse_err <= LSE_TOL
 
 
 @pytest.mark.parametrize("causal,N,H", [(True, 8192, 2), (False, 4096, 1)],

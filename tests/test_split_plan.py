@@ -83,11 +83,14 @@ def check_plan(pl, B, H, N, D, causal):
     ("C3", 4, 32, 4096, 128, 0, A.FA_DTYPE_F16, False),
     ("C4", 2, 32, 8192, 128, 1, A.FA_DTYPE_BF16, False),
     ("C5", 1, 16, 16384, 128, 1, A.FA_DTYPE_F16, False),
-    ("C5r", 1, 16, 3000, 128, 1, A.FA_DTYPE_F16, True),
+    ("C5r", 1, 16, 3000, 128, 1, A.FA_DTYPE_F16, False),
+    ("C5r/2", 1, 8, 3000, 128, 1, A.FA_DTYPE_F16, True),
 ])
 def test_baseline_configs(lib, name, B, H, N, D, causal, dtype, split):
-    """The full-machine configurations run unsplit (nothing to gain); the
-    short causal C5r splits its long q-tiles."""
+    """The BASELINE configurations run unsplit: C2-C5 fill the machine, and
+    C5r's longest q-tile (47 key tiles) is within 1.5x of the throughput
+    bound (9584 tiles over 256 CUs x 1.1), where the partials' cost ate the
+    measured gain.  With half its heads the same shape splits."""
     p = contiguous(B=B, H=H, N=N, D=D, dtype=dtype, causal=causal)
     pl = plan(lib, p)
     assert pl.block_rows == (256 if (N >= 2048 and not causal) or
@@ -98,16 +101,18 @@ def test_baseline_configs(lib, name, B, H, N, D, causal, dtype, split):
         check_plan(pl, B, H, N, D, causal)
 
 
-def test_c5r_plan_shape(lib):
-    """C5r on 256 CUs: 24 q-tiles of 2..47 key tiles; average load per
-    workgroup slot 16*599/512 = 18.7 tiles, so chunks of at most 19 tiles:
-    q-tiles of 20..38 tiles in 2 chunks, 40..47 in 3."""
-    pl = plan(lib, contiguous(B=1, H=16, N=3000, D=128, causal=1))
-    check_plan(pl, 1, 16, 3000, 128, 1)
+def test_c5r_half_heads_plan_shape(lib):
+    """B1 H8 N3000 causal on 256 CUs: 24 q-tiles of 2, 4, ..., 46, 47 key
+    tiles.  Throughput bound 8*599/(256*1.1) = 17.0 tiles < 47 / 1.5 - 8:
+    split.  Average load per workgroup slot 8*599/512 = 9.4 tiles, so chunks
+    of at most S = 10 tiles: q-tiles of 12..20 tiles in 2 chunks, 22..30 in
+    3, 32..40 in 4, 42..47 in 5."""
+    pl = plan(lib, contiguous(B=1, H=8, N=3000, D=128, causal=1))
+    check_plan(pl, 1, 8, 3000, 128, 1)
     assert pl.block_rows == 128
-    assert pl.n_merge == 15 and pl.n_slots == 10 * 2 + 5 * 3
-    assert pl.n_items == 9 + 20 + 15
-    assert max(pl.tile_end[i] - pl.tile_begin[i] for i in range(pl.n_items)) == 19
+    assert pl.n_merge == 19 and pl.n_slots == 5 * 2 + 5 * 3 + 5 * 4 + 4 * 5
+    assert pl.n_items == 5 + 10 + 15 + 20 + 20
+    assert max(pl.tile_end[i] - pl.tile_begin[i] for i in range(pl.n_items)) == 10
 
 
 @pytest.mark.parametrize("B,H,N,D,causal,dtype", [
@@ -147,17 +152,17 @@ def test_plan_sweep(lib, N, causal, H):
 def test_more_cus_split_more(lib):
     """The split is a response to idle CUs: a machine with fewer CUs runs the
     same problem unsplit, a larger one splits it."""
-    p = contiguous(B=1, H=16, N=3000, D=128, causal=1)
+    p = contiguous(B=1, H=8, N=3000, D=128, causal=1)
     assert plan(lib, p, cus=8).n_items == 0
     assert plan(lib, p, cus=256).n_items > 0
     big = plan(lib, p, cus=1024)
-    check_plan(big, 1, 16, 3000, 128, 1)
+    check_plan(big, 1, 8, 3000, 128, 1)
     assert big.n_slots >= plan(lib, p, cus=256).n_slots
 
 
 def test_plan_ignores_pointers_and_lse(lib):
-    p1 = contiguous(B=1, H=16, N=3000, D=128, causal=1)
-    p2 = contiguous(B=1, H=16, N=3000, D=128, causal=1, lse=False)
+    p1 = contiguous(B=1, H=8, N=3000, D=128, causal=1)
+    p2 = contiguous(B=1, H=8, N=3000, D=128, causal=1, lse=False)
     p2.q = 0x7000000
     a, b = plan(lib, p1), plan(lib, p2)
     assert bytes(a) == bytes(b)
