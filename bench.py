@@ -18,6 +18,7 @@ benchmark/cpp/correctness_v6.cu:23-72, restated in oracle/attn_oracle.c)
 timed on a bounded sample of rows of the same workload on the host cores.
 
 --all additionally times every BASELINE config and prints a table to stderr.
+--split-table times few-head shapes with and without split-KV instead.
 """
 from __future__ import annotations
 
@@ -43,6 +44,15 @@ WORKLOADS = {
     "C5": (1, 16, 16384, 128, "fp16", True, 3.0, 4),
     "C5r": (1, 16, 3000, 128, "fp16", True, 3.0, 5),
 }
+# Few-head shapes that leave most CUs idle unsplit (the target of split-KV;
+# not BASELINE configs): timed with and without the split by --split-table.
+SPLIT_SHAPES = {
+    "S1": (1, 1, 4096, 128, "fp16", False, 1.0, 11),
+    "S2": (1, 4, 8192, 128, "fp16", True, 1.0, 12),
+    "S3": (1, 8, 3000, 128, "fp16", True, 3.0, 13),
+    "S4": (1, 2, 8192, 128, "bf16", True, 1.0, 14),
+    "S5": (2, 4, 2048, 64, "fp16", False, 1.0, 15),
+}
 TRAFFIC_FILE = os.path.join(REPO_ROOT, "profiles", "fa_fwd_C3_traffic.json")
 
 
@@ -54,7 +64,7 @@ def flops(B, H, N, D, causal):
 def make_inputs(torch, name, device, input_mode="random"):
     from fa_bench.input_data import generate_qkv
 
-    B, H, N, D, dtype, causal, sigma, case = WORKLOADS[name]
+    B, H, N, D, dtype, causal, sigma, case = {**WORKLOADS, **SPLIT_SHAPES}[name]
     td = {"fp16": torch.float16, "bf16": torch.bfloat16}[dtype]
     q, k, v, _ = generate_qkv(batch_size=B, n_heads=H, seq_len=N, d_head=D, dtype=td,
                               device=device, input_mode=input_mode, seed=1234, case_index=case,
@@ -62,11 +72,11 @@ def make_inputs(torch, name, device, input_mode="random"):
     return (q, k, v), causal
 
 
-def time_workload(torch, fa, name, steps, warmup, input_mode="random"):
+def time_workload(torch, fa, name, steps, warmup, input_mode="random", split_kv=True):
     (q, k, v), causal = make_inputs(torch, name, "cuda", input_mode)
     o = torch.empty_like(q)
     for _ in range(warmup):
-        fa.forward(q, k, v, o, causal=causal)
+        fa.forward(q, k, v, o, causal=causal, split_kv=split_kv)
     stream = torch.cuda.current_stream()
     start = torch.cuda.Event(enable_timing=True)
     stop = torch.cuda.Event(enable_timing=True)
@@ -74,7 +84,7 @@ def time_workload(torch, fa, name, steps, warmup, input_mode="random"):
     t0 = time.perf_counter()
     start.record(stream)
     for _ in range(steps):
-        fa.forward(q, k, v, o, causal=causal)
+        fa.forward(q, k, v, o, causal=causal, split_kv=split_kv)
     stop.record(stream)
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3
@@ -237,6 +247,9 @@ def main():
     ap.add_argument("--workload", default="C3", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--all", action="store_true", help="also time every config (stderr table)")
+    ap.add_argument("--split-table", action="store_true",
+                    help="instead of the metric, time the few-head shapes with and without "
+                         "split-KV (stderr table)")
     ap.add_argument("--input-mode", default="random", choices=["random", "structured", "stress"],
                     help="input values (the headline metric is quoted on random)")
     ap.add_argument("--gemm-ceiling", action="store_true",
@@ -282,6 +295,20 @@ def main():
 
     if args.gemm_ceiling:
         gemm_ceiling(torch, args.steps, args.warmup)
+        return
+
+    if args.split_table:
+        print(f"{'shape':5s} {'B':>2s} {'H':>3s} {'N':>6s} {'D':>4s} {'dtype':>5s} {'mask':>7s} "
+              f"{'unsplit ms':>11s} {'split ms':>9s} {'speed-up':>9s} {'split TFLOPS':>13s}",
+              file=sys.stderr, flush=True)
+        for sn, (B, H, N, D, dt, causal, _, _) in SPLIT_SHAPES.items():
+            u_ms, _, _ = time_workload(torch, fa, sn, args.steps, args.warmup, args.input_mode,
+                                       split_kv=False)
+            s_ms, s_tf, _ = time_workload(torch, fa, sn, args.steps, args.warmup,
+                                          args.input_mode, split_kv=True)
+            print(f"{sn:5s} {B:2d} {H:3d} {N:6d} {D:4d} {dt:>5s} "
+                  f"{'causal' if causal else 'none':>7s} {u_ms:11.4f} {s_ms:9.4f} "
+                  f"{u_ms / s_ms:8.2f}x {s_tf:13.1f}", file=sys.stderr, flush=True)
         return
 
     name = args.workload

@@ -85,3 +85,22 @@ def test_mfma_probe_reaches_formula_peak():
     assert rows[("ones", 1)][1] > 85.0, rows
     for tflops, pct in rows.values():
         assert 0.0 < pct <= 101.0 and tflops > 0.0
+
+
+def test_bench_split_table():
+    """bench.py --split-table times every few-head shape with and without
+    split-KV; the split must not lose on any of them."""
+    import sys
+
+    print("case bench --split-table", flush=True)
+    r = subprocess.run([sys.executable, os.path.join(REPO, "bench.py"), "--split-table",
+                        "--steps", "10", "--warmup", "2"], capture_output=True, text=True,
+                       timeout=240)
+    assert r.returncode == 0, r.stderr[-2000:]
+    rows = [ln.split() for ln in r.stderr.splitlines() if ln[:2] in ("S1", "S2", "S3", "S4", "S5")]
+    print("\n".join(" ".join(x) for x in rows), flush=True)
+    assert [x[0] for x in rows] == ["S1", "S2", "S3", "S4", "S5"]
+    for x in rows:
+        unsplit, split = float(x[7]), float(x[8])
+        assert unsplit > 0 and split > 0
+        assert split < 1.05 * unsplit, x
