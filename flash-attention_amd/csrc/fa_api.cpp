@@ -99,6 +99,7 @@ void to_kernel_args(const fa_fwd_params* p, fa::KernelArgs* a) {
   a->split.n_items = 0;
   a->split.n_slots = 0;
   a->split.n_merge = 0;
+  a->split.xcd_heads = 0;
 }
 
 // Compute units of the calling thread's current device (queried once per
@@ -124,20 +125,21 @@ fa_status current_compute_units(int* cus) {
   return FA_OK;
 }
 
-// Validates p and launches it, split over the workspace when the plan for
-// the current device asks for one and a workspace is given (workspace ==
-// NULL: never split, the plain fa_fwd path).
+// Validates p and launches it with the work plan for the current device:
+// split over the workspace when the plan asks for one and a workspace is
+// given (workspace == NULL: never split, the plain fa_fwd path), else
+// possibly an XCD placement table (no workspace, same arithmetic).
 fa_status launch(const fa_fwd_params* p, void* workspace, uint64_t workspace_bytes,
                  void* stream) {
   const fa_status s = fa_fwd_validate(p);
   if (s != FA_OK) return s;
   fa::KernelArgs a;
   to_kernel_args(p, &a);
-  if (workspace != nullptr) {
+  {
     int cus = 0;
     const fa_status st = current_compute_units(&cus);
     if (st != FA_OK) return st;
-    const size_t need = fa::plan_split(a, cus, &a.split);
+    const size_t need = fa::plan_split(a, cus, workspace != nullptr, &a.split);
     if (need > 0) {
       if (workspace_bytes < need)
         return fail(FA_ERR_ARG, "workspace of %llu bytes is smaller than the %llu bytes needed",
@@ -261,11 +263,12 @@ fa_status fa_fwd_plan(const fa_fwd_params* p, int32_t compute_units, fa_fwd_plan
     return fail(FA_ERR_ARG, "compute_units must be >= 1 (got %d)", (int)compute_units);
   fa::KernelArgs a;
   to_kernel_args(p, &a);
-  out->workspace_bytes = fa::plan_split(a, compute_units, &a.split);
+  out->workspace_bytes = fa::plan_split(a, compute_units, true, &a.split);
   out->block_rows = fa::block_rows(a);
   out->n_items = a.split.n_items;
   out->n_slots = a.split.n_slots;
   out->n_merge = a.split.n_merge;
+  out->xcd_heads = a.split.xcd_heads;
   for (int i = 0; i < a.split.n_items; ++i) {
     const uint32_t info = a.split.item[i];
     const int qb = (int)(info & 0xffffu), c = (int)((info >> 16) & 0xffu), nch = (int)(info >> 24);
@@ -277,6 +280,7 @@ fa_status fa_fwd_plan(const fa_fwd_params* p, int32_t compute_units, fa_fwd_plan
     out->tile_begin[i] = (int32_t)((int64_t)c * T / nch);
     out->tile_end[i] = (int32_t)((int64_t)(c + 1) * T / nch);
     out->slot[i] = nch > 1 ? a.split.slot[i] + c : -1;
+    out->head[i] = a.split.xcd_heads > 0 ? a.split.slot[i] : -1;
   }
   return FA_OK;
 }
@@ -291,7 +295,7 @@ fa_status fa_fwd_workspace_size(const fa_fwd_params* p, uint64_t* bytes) {
   if (st != FA_OK) return st;
   fa::KernelArgs a;
   to_kernel_args(p, &a);
-  *bytes = fa::plan_split(a, cus, &a.split);
+  *bytes = fa::plan_split(a, cus, true, &a.split);
   return FA_OK;
 }
 

@@ -10,21 +10,31 @@
 
 namespace fa {
 
+// Work plan of a launch, computed on the host (plan_split).
+//
 // Split-KV: long key ranges of a q-tile are cut into chunks computed by
 // separate workgroups, whose partial results (unnormalised fp32 O, offset m
 // and row sum l per row) go to a caller-provided workspace and are merged by
 // a second kernel.  Used when the grid would leave most of the machine idle
 // behind a few long q-tiles (short causal problems, few heads).
+//
+// XCD placement table (xcd_heads > 0, no chunks, no workspace): a causal
+// grid of one round of two workgroups per CU, where the hardware puts the
+// k-th and (k + CUs per XCD)-th workgroups of an XCD on the same CU.  The
+// table orders each XCD's q-tiles so the longest run alone and the others
+// share a CU long with short.
 constexpr int kMaxSplitItems = 128;
 
 struct SplitPlan {
   int32_t n_items;   // work items per (batch, head); 0: no split
   int32_t n_slots;   // partial-result slots per (batch, head)
   int32_t n_merge;   // q-tiles with more than one chunk (merged by the second kernel)
+  int32_t xcd_heads; // > 0: XCD placement table over this many heads per XCD
   // Item i: q-tile (bits 0..15), chunk (16..23), chunk count (24..31).
   uint32_t item[kMaxSplitItems];
   // Item i's first partial slot of its q-tile (items of one q-tile use
-  // slot[i] + chunk); unused for single-chunk items.
+  // slot[i] + chunk); unused for single-chunk items.  In the XCD placement
+  // table: the head (within the XCD's heads) of dispatch position i.
   uint16_t slot[kMaxSplitItems];
   // Merge list: q-tile (bits 0..15) | chunk count (16..23), first slot in merge_slot.
   uint32_t merge[kMaxSplitItems];
@@ -57,9 +67,11 @@ struct KernelArgs {
 // Workgroup rows (BM) of the kernel variant launch_fwd picks for args.
 int block_rows(const KernelArgs& args);
 
-// Computes the split plan for args on a device with `compute_units` CUs.
-// Returns the workspace bytes it needs (0: no split; plan->n_items = 0).
-size_t plan_split(const KernelArgs& args, int compute_units, SplitPlan* plan);
+// Computes the work plan for args on a device with `compute_units` CUs.
+// With allow_split it may choose split-KV and returns the workspace bytes it
+// needs; otherwise (or when no split pays) it returns 0 and leaves either no
+// plan (n_items = 0) or an XCD placement table (xcd_heads > 0).
+size_t plan_split(const KernelArgs& args, int compute_units, bool allow_split, SplitPlan* plan);
 
 // Launches the forward kernel for args (validated by the caller) on stream.
 // With args.split.n_items > 0 (and the workspace set) it launches the split

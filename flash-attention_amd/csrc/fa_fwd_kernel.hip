@@ -189,12 +189,21 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
   const int hg = (lane >> 4) & 1;  // 16-lane group within the half
 
   const int N = args.seq_len;
-  const int logical = xcd_remap(blockIdx.x, gridDim.x);
-  // Work item of this workgroup: a q-tile, or with split-KV one chunk of a
-  // q-tile's key tiles (the plan lists items longest first).
-  const int per_bh = SPLIT ? args.split.n_items : args.n_qblocks;
-  const int bh = logical / per_bh;
-  const int item = logical - bh * per_bh;
+  // Work item of this workgroup: a q-tile, or with a plan one entry of its
+  // table: a chunk of a q-tile's key tiles (split-KV; the plan lists items
+  // longest first), or the q-tile of this dispatch position within its XCD
+  // (XCD placement table).
+  int bh, item;
+  if (SPLIT && args.split.xcd_heads > 0) {
+    // Hardware dispatch: workgroup b runs on XCD b % 8 as its (b / 8)-th.
+    item = (int)(blockIdx.x >> 3);
+    bh = (int)(blockIdx.x & 7) * args.split.xcd_heads + args.split.slot[item];
+  } else {
+    const int logical = xcd_remap(blockIdx.x, gridDim.x);
+    const int per_bh = SPLIT ? args.split.n_items : args.n_qblocks;
+    bh = logical / per_bh;
+    item = logical - bh * per_bh;
+  }
   int qb, chunk = 0, n_chunks = 1;
   if constexpr (SPLIT) {
     const uint32_t info = args.split.item[item];
@@ -654,12 +663,18 @@ hipError_t launch_one(const KernelArgs& a, hipStream_t stream) {
   constexpr int BM = 32 * NW;
   KernelArgs args = a;
   args.n_qblocks = (args.seq_len + BM - 1) / BM;
-  // A split plan is only valid for the block height it was made for.
-  if (args.split.n_items > 0 && (block_rows(args) != BM || args.ws_o == nullptr ||
-                                 args.ws_ml == nullptr || args.split.n_items > kMaxSplitItems))
-    return hipErrorInvalidValue;
+  // A plan is only valid for the block height it was made for; partials
+  // need the workspace; a placement table covers 8 XCDs of whole heads.
   const int64_t bh = (int64_t)args.batch * args.heads;
-  const int64_t total = (args.split.n_items > 0 ? args.split.n_items : args.n_qblocks) * bh;
+  const SplitPlan& sp = args.split;
+  if (sp.n_items > 0 &&
+      (block_rows(args) != BM || sp.n_items > kMaxSplitItems ||
+       (sp.n_merge > 0 && (args.ws_o == nullptr || args.ws_ml == nullptr)) ||
+       (sp.xcd_heads > 0 && (sp.n_merge > 0 || bh != 8 * (int64_t)sp.xcd_heads ||
+                             sp.n_items != sp.xcd_heads * args.n_qblocks))))
+    return hipErrorInvalidValue;
+  const int64_t total = sp.xcd_heads > 0 ? 8 * (int64_t)sp.n_items
+                                         : (sp.n_items > 0 ? sp.n_items : args.n_qblocks) * bh;
   if (total > 0x7fffffff) return hipErrorInvalidValue;
   if (args.split.n_items == 0) {
     hipLaunchKernelGGL((fa_fwd_kernel<D, BF16, CAUSAL, NW, false>), dim3((unsigned)total),
@@ -669,7 +684,7 @@ hipError_t launch_one(const KernelArgs& a, hipStream_t stream) {
   hipLaunchKernelGGL((fa_fwd_kernel<D, BF16, CAUSAL, NW, true>), dim3((unsigned)total),
                      dim3(NW * 64), 0, stream, args);
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
+  if (e != hipSuccess || sp.n_merge == 0) return e;
   constexpr int RPB = 256 / (D / 4);
   const int64_t merge_blocks = bh * args.split.n_merge * ((BM + RPB - 1) / RPB);
   if (merge_blocks > 0x7fffffff) return hipErrorInvalidValue;
@@ -705,17 +720,22 @@ int block_rows(const KernelArgs& a) {
   return a.seq_len >= kWideMinSeq ? 256 : 128;
 }
 
-size_t plan_split(const KernelArgs& a, int compute_units, SplitPlan* plan) {
-  plan->n_items = plan->n_slots = plan->n_merge = 0;
-  constexpr int BN = 64;
+namespace {
+
+constexpr int kKeyTile = 64;  // keys per K/V tile (Tile<D>::BN)
+
+// Key tiles of q-tile qb.
+int q_tile_tiles(const KernelArgs& a, int BM, int qb) {
+  const int kv = a.causal ? std::min(a.seq_len, (qb + 1) * BM) : a.seq_len;
+  return (kv + kKeyTile - 1) / kKeyTile;
+}
+
+// Split-KV plan, or 0 items when no split pays (see plan_split).
+size_t plan_chunks(const KernelArgs& a, int compute_units, SplitPlan* plan) {
   const int BM = block_rows(a);
-  const int N = a.seq_len;
-  const int nq = (N + BM - 1) / BM;
-  if (compute_units < 1 || nq > kMaxSplitItems) return 0;
-  auto tiles = [&](int qb) {
-    const int kv = a.causal ? std::min(N, (qb + 1) * BM) : N;
-    return (kv + BN - 1) / BN;
-  };
+  const int nq = (a.seq_len + BM - 1) / BM;
+  if (nq > kMaxSplitItems) return 0;
+  auto tiles = [&](int qb) { return q_tile_tiles(a, BM, qb); };
   // Workgroup slots of the machine: two 4-wave workgroups or one 8-wave
   // workgroup per CU.  The unsplit grid finishes no earlier than its longest
   // q-tile (t_max key tiles) and no earlier than the total load over the
@@ -781,6 +801,63 @@ size_t plan_split(const KernelArgs& a, int compute_units, SplitPlan* plan) {
   plan->n_merge = n_merge;
   // Partial O (fp32) then (m, l) per row of every slot.
   return (size_t)a.batch * a.heads * n_slots * BM * ((size_t)a.head_dim * 4 + 8);
+}
+
+// XCD placement table for a causal 4-wave grid of one round: each XCD
+// (cpx CUs) receives n = heads_per_xcd * nq workgroups, cpx < n <= 2 cpx.
+// Measured dispatch (per-workgroup hardware CU ids): an XCD's k-th
+// workgroup goes to CU slot k mod cpx, so positions k and k + cpx share a
+// CU for k < n - cpx, and positions n - cpx .. cpx - 1 run alone.  Longest
+// first (the default order) pairs the longest q-tile with the (cpx+1)-th
+// longest: at B1 H16 N3000 the 47-tile q-tile shared its CU with a 32-tile
+// one and set the kernel time (66 us).  The table gives the alone
+// positions the longest q-tiles and pairs the rest longest with shortest.
+void plan_xcd_table(const KernelArgs& a, int compute_units, SplitPlan* plan) {
+  const int BM = block_rows(a);
+  if (!a.causal || BM != 128 || compute_units % 8 != 0) return;
+  const int64_t bh = (int64_t)a.batch * a.heads;
+  if (bh % 8 != 0) return;
+  const int nq = (a.seq_len + BM - 1) / BM;
+  const int64_t hpx = bh / 8;
+  const int64_t cpx = compute_units / 8;
+  const int64_t n = hpx * nq;
+  if (n <= cpx || n > 2 * cpx || n > kMaxSplitItems) return;
+  struct Entry { int len, qb, head; };
+  Entry all[kMaxSplitItems];
+  int k = 0;
+  for (int h = 0; h < (int)hpx; ++h)
+    for (int qb = 0; qb < nq; ++qb) all[k++] = Entry{q_tile_tiles(a, BM, qb), qb, h};
+  std::stable_sort(all, all + n, [](const Entry& x, const Entry& y) {
+    return x.len != y.len ? x.len > y.len : x.qb > y.qb;
+  });
+  const int m = (int)(n - cpx);      // shared CUs
+  const int alone = (int)(cpx - m);  // CUs with one workgroup
+  // all[0, alone): alone positions [m, cpx); all[alone, n): pairs, the
+  // j-th longest of them at position j, the j-th shortest at cpx + j.
+  for (int pos = 0; pos < (int)n; ++pos) {
+    int src;
+    if (pos < m) src = alone + pos;
+    else if (pos < (int)cpx) src = pos - m;
+    else src = (int)n - 1 - (pos - (int)cpx);
+    plan->item[pos] = (uint32_t)all[src].qb | (1u << 24);  // chunk 0 of 1
+    plan->slot[pos] = (uint16_t)all[src].head;
+  }
+  plan->n_items = (int)n;
+  plan->xcd_heads = (int)hpx;
+}
+
+}  // namespace
+
+size_t plan_split(const KernelArgs& a, int compute_units, bool allow_split, SplitPlan* plan) {
+  plan->n_items = plan->n_slots = plan->n_merge = plan->xcd_heads = 0;
+  if (compute_units < 1) return 0;
+  if (allow_split) {
+    const size_t bytes = plan_chunks(a, compute_units, plan);
+    if (bytes > 0) return bytes;
+    plan->n_items = plan->n_slots = plan->n_merge = 0;
+  }
+  plan_xcd_table(a, compute_units, plan);
+  return 0;
 }
 
 hipError_t launch_fwd(const KernelArgs& a, hipStream_t stream) {

@@ -111,15 +111,21 @@ typedef struct {
   int32_t n_items;          /* workgroups per (batch, head); 0: the problem runs unsplit */
   int32_t n_slots;          /* partial-result slots per (batch, head) in the workspace */
   int32_t n_merge;          /* q-tiles with more than one chunk (merged by a second kernel) */
+  int32_t xcd_heads;        /* > 0: XCD placement table (no split) over this many heads per XCD */
   uint64_t workspace_bytes; /* bytes fa_fwd_ws needs (0 when unsplit) */
-  /* Work item i (dispatch order, longest first): q-tile q_tile[i], key tiles
-   * (64 keys each) [tile_begin[i], tile_end[i]) of its n_chunks[i] chunks,
-   * partial slot slot[i] (-1 for a q-tile of one chunk, stored directly). */
+  /* Split-KV (xcd_heads == 0): work item i (dispatch order, longest first)
+   * of every (batch, head) is q-tile q_tile[i], key tiles (64 keys each)
+   * [tile_begin[i], tile_end[i]) of its n_chunks[i] chunks, partial slot
+   * slot[i] (-1 for a q-tile of one chunk, stored directly).
+   * XCD placement table (xcd_heads > 0): the i-th workgroup dispatched to
+   * each XCD runs q-tile q_tile[i] of head head[i] among that XCD's
+   * xcd_heads heads, all its key tiles.  fa_fwd uses the same table. */
   int32_t q_tile[FA_PLAN_MAX_ITEMS];
   int32_t tile_begin[FA_PLAN_MAX_ITEMS];
   int32_t tile_end[FA_PLAN_MAX_ITEMS];
   int32_t n_chunks[FA_PLAN_MAX_ITEMS];
   int32_t slot[FA_PLAN_MAX_ITEMS];
+  int32_t head[FA_PLAN_MAX_ITEMS];
 } fa_fwd_plan_t;
 
 /* Host-only argument check; touches no GPU.  Returns FA_OK or the first
@@ -154,8 +160,9 @@ fa_status fa_fwd_ws(const fa_fwd_params* p, void* workspace, uint64_t workspace_
 fa_status fa_fwd_ws_timed(const fa_fwd_params* p, void* workspace, uint64_t workspace_bytes,
                           void* stream, float* ms);
 
-/* The split plan fa_fwd_ws would use for *p on a device with
- * `compute_units` CUs.  Host only; touches no GPU. */
+/* The work plan fa_fwd_ws would use for *p on a device with
+ * `compute_units` CUs (split-KV, or an XCD placement table, or none).
+ * Host only; touches no GPU. */
 fa_status fa_fwd_plan(const fa_fwd_params* p, int32_t compute_units, fa_fwd_plan_t* out);
 
 /* Static description of a status code. */

@@ -66,12 +66,14 @@ class FaFwdPlan(ctypes.Structure):
         ("n_items", ctypes.c_int32),
         ("n_slots", ctypes.c_int32),
         ("n_merge", ctypes.c_int32),
+        ("xcd_heads", ctypes.c_int32),
         ("workspace_bytes", ctypes.c_uint64),
         ("q_tile", ctypes.c_int32 * FA_PLAN_MAX_ITEMS),
         ("tile_begin", ctypes.c_int32 * FA_PLAN_MAX_ITEMS),
         ("tile_end", ctypes.c_int32 * FA_PLAN_MAX_ITEMS),
         ("n_chunks", ctypes.c_int32 * FA_PLAN_MAX_ITEMS),
         ("slot", ctypes.c_int32 * FA_PLAN_MAX_ITEMS),
+        ("head", ctypes.c_int32 * FA_PLAN_MAX_ITEMS),
     ]
 
 

@@ -109,9 +109,9 @@ int main(void) {
   F(fa_device_info_t, memory_clock_khz); F(fa_device_info_t, fp16_dense_peak_tflops);
   F(fa_device_info_t, hbm_peak_gbps);
   F(fa_fwd_plan_t, block_rows); F(fa_fwd_plan_t, n_items); F(fa_fwd_plan_t, n_slots);
-  F(fa_fwd_plan_t, n_merge); F(fa_fwd_plan_t, workspace_bytes); F(fa_fwd_plan_t, q_tile);
-  F(fa_fwd_plan_t, tile_begin); F(fa_fwd_plan_t, tile_end); F(fa_fwd_plan_t, n_chunks);
-  F(fa_fwd_plan_t, slot);
+  F(fa_fwd_plan_t, n_merge); F(fa_fwd_plan_t, xcd_heads); F(fa_fwd_plan_t, workspace_bytes);
+  F(fa_fwd_plan_t, q_tile); F(fa_fwd_plan_t, tile_begin); F(fa_fwd_plan_t, tile_end);
+  F(fa_fwd_plan_t, n_chunks); F(fa_fwd_plan_t, slot); F(fa_fwd_plan_t, head);
   printf("\"sizeof.fa_fwd_params\": [%zu, 0], \"sizeof.fa_device_info_t\": [%zu, 0], "
          "\"sizeof.fa_fwd_plan_t\": [%zu, 0]}\n",
          sizeof(fa_fwd_params), sizeof(fa_device_info_t), sizeof(fa_fwd_plan_t));

@@ -319,3 +319,29 @@ def test_abi_unsplit_problem_needs_no_workspace(fa, lib):
     assert lib.fa_fwd_ws(ctypes.byref(p), None, 0, _stream()) == A.FA_OK
     torch.cuda.synchronize()
     assert torch.equal(o, fa.forward(q, k, v, causal=causal))
+
+
+def test_xcd_table_c5r_bitwise_equals_plain_order(fa, lib, cus):
+    """C5r runs with the XCD placement table (a dispatch order only): every
+    head's output and LSE are bit for bit those of the same heads run in
+    the plain longest-first order (4 heads per call, no table, no split)."""
+    _note("case XCD table C5r")
+    q, k, v, causal, _ = make_config("C5r", device=DEV)
+    pl = _plan(lib, cus, q, k, v, torch.empty_like(q), causal)
+    _note(f"  plan: xcd_heads={pl.xcd_heads} items={pl.n_items}")
+    if cus == 256:
+        assert pl.xcd_heads == 2 and pl.n_items == 48 and pl.n_merge == 0
+    o, lse = fa.forward(q, k, v, causal=True, return_lse=True)
+    o2, lse2 = fa.forward(q, k, v, causal=True, return_lse=True, split_kv=False)
+    torch.cuda.synchronize()
+    assert torch.equal(o, o2) and torch.equal(lse, lse2)
+    for h in range(0, q.shape[1], 4):
+        sl = slice(h, h + 4)
+        p4 = _plan(lib, cus, q[:, sl], k[:, sl], v[:, sl], torch.empty_like(q[:, sl]), causal)
+        assert p4.xcd_heads == 0
+        ph, lh = fa.forward(q[:, sl], k[:, sl], v[:, sl], causal=True, return_lse=True,
+                            split_kv=False)
+        torch.cuda.synchronize()
+        assert p4.n_items == 0 or p4.n_merge > 0  # plain order (no table) without split
+        assert torch.equal(o[:, sl], ph), f"heads {h}..{h + 3}"
+        assert torch.equal(lse[:, sl], lh)

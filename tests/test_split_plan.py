@@ -37,6 +37,35 @@ def tiles(qb, N, BM, causal):
     return (kv + BN - 1) // BN
 
 
+def check_table(pl, B, H, N, causal, cus=256):
+    """XCD placement table: a permutation of one XCD's (head, q-tile) pairs
+    whose alone positions hold the longest q-tiles and whose shared CUs
+    pair long with short."""
+    BM = pl.block_rows
+    nq = (N + BM - 1) // BM
+    hpx, cpx = B * H // 8, cus // 8
+    n = pl.n_items
+    assert causal and BM == 128 and B * H == 8 * pl.xcd_heads == 8 * hpx
+    assert n == hpx * nq and cpx < n <= 2 * cpx
+    assert pl.n_merge == 0 and pl.n_slots == 0 and pl.workspace_bytes == 0
+    pairs = sorted((pl.head[i], pl.q_tile[i]) for i in range(n))
+    assert pairs == [(h, q) for h in range(hpx) for q in range(nq)]
+    for i in range(n):
+        assert pl.n_chunks[i] == 1 and pl.slot[i] == -1 and pl.tile_begin[i] == 0
+        assert pl.tile_end[i] == tiles(pl.q_tile[i], N, BM, causal)
+    lens = [pl.tile_end[i] for i in range(n)]
+    m = n - cpx
+    alone = lens[m:cpx]
+    shared = [(lens[j], lens[cpx + j]) for j in range(m)]
+    if alone:
+        assert min(alone) >= max(max(a, b) for a, b in shared)
+    # long with short: the j-th longest first occupant meets the j-th shortest second
+    firsts = [a for a, _ in shared]
+    seconds = [b for _, b in shared]
+    assert firsts == sorted(firsts, reverse=True) and seconds == sorted(seconds)
+    assert min(firsts) >= max(seconds)
+
+
 def check_plan(pl, B, H, N, D, causal):
     BM = pl.block_rows
     nq = (N + BM - 1) // BM
@@ -83,22 +112,38 @@ def check_plan(pl, B, H, N, D, causal):
     ("C3", 4, 32, 4096, 128, 0, A.FA_DTYPE_F16, False),
     ("C4", 2, 32, 8192, 128, 1, A.FA_DTYPE_BF16, False),
     ("C5", 1, 16, 16384, 128, 1, A.FA_DTYPE_F16, False),
-    ("C5r", 1, 16, 3000, 128, 1, A.FA_DTYPE_F16, False),
+    ("C5r", 1, 16, 3000, 128, 1, A.FA_DTYPE_F16, "table"),
     ("C5r/2", 1, 8, 3000, 128, 1, A.FA_DTYPE_F16, True),
 ])
 def test_baseline_configs(lib, name, B, H, N, D, causal, dtype, split):
     """The BASELINE configurations run unsplit: C2-C5 fill the machine, and
     C5r's longest q-tile (47 key tiles) is within 1.5x of the throughput
     bound (9584 tiles over 256 CUs x 1.1), where the partials' cost ate the
-    measured gain.  With half its heads the same shape splits."""
+    measured gain; C5r gets the XCD placement table instead (48 q-tiles per
+    XCD on 32 CUs).  With half its heads the same shape splits."""
     p = contiguous(B=B, H=H, N=N, D=D, dtype=dtype, causal=causal)
     pl = plan(lib, p)
     assert pl.block_rows == (256 if (N >= 2048 and not causal) or
                              (causal and dtype == A.FA_DTYPE_F16 and N >= 8192) else 128)
-    if not split:
+    if split == "table":
+        assert pl.xcd_heads == 2
+        check_table(pl, B, H, N, causal)
+    elif not split:
         assert pl.n_items == 0 and pl.workspace_bytes == 0 and pl.n_slots == 0
     else:
+        assert pl.xcd_heads == 0
         check_plan(pl, B, H, N, D, causal)
+
+
+def test_c5r_table_shape(lib):
+    """C5r: 2 heads x 24 q-tiles per XCD, 32 CUs: 16 shared CUs, 16 alone.
+    The 16 longest q-tiles (47, 47, 46, 46, ..., 34, 34 key tiles) run alone;
+    the 32-tile ones share with the 2-tile ones."""
+    pl = plan(lib, contiguous(B=1, H=16, N=3000, D=128, causal=1))
+    lens = [pl.tile_end[i] for i in range(pl.n_items)]
+    assert pl.n_items == 48
+    assert sorted(lens[16:32]) == sorted([47, 47] + [2 * q for q in range(17, 24) for _ in (0, 1)])
+    assert (lens[0], lens[32]) == (32, 2) and (lens[15], lens[47]) == (18, 16)
 
 
 def test_c5r_half_heads_plan_shape(lib):
@@ -128,6 +173,7 @@ def test_c5r_half_heads_plan_shape(lib):
 def test_split_plans_are_complete(lib, B, H, N, D, causal, dtype):
     pl = plan(lib, contiguous(B=B, H=H, N=N, D=D, dtype=dtype, causal=causal))
     BM = pl.block_rows
+    assert pl.xcd_heads == 0
     if (N + BM - 1) // BM >= A.FA_PLAN_MAX_ITEMS:
         assert pl.n_items == 0  # no item left for a second chunk: never split
         return
@@ -143,7 +189,9 @@ def test_plan_sweep(lib, N, causal, H):
     for D in (64, 128):
         for dtype in (A.FA_DTYPE_F16, A.FA_DTYPE_BF16):
             pl = plan(lib, contiguous(B=1, H=H, N=N, D=D, dtype=dtype, causal=causal))
-            if pl.n_items:
+            if pl.xcd_heads:
+                check_table(pl, 1, H, N, causal)
+            elif pl.n_items:
                 check_plan(pl, 1, H, N, D, causal)
             else:
                 assert pl.workspace_bytes == 0 and pl.n_merge == 0 and pl.n_slots == 0
