@@ -212,6 +212,16 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
     n_chunks = (int)(info >> 24);
   } else {
     qb = CAUSAL ? args.n_qblocks - 1 - item : item;  // longest q-tiles first
+    if (CAUSAL && ((args.batch * args.heads) & 7) == 0) {
+      // Whole heads per XCD: longest first across the XCD's heads (their
+      // q-tiles interleaved), not head after head, so the last head's long
+      // q-tiles do not start late (+1.5 % at B2 H32 N8192 and B1 H16
+      // N16384, +2.7 % at B1 H16 N8192).  Same blocks per XCD as xcd_remap.
+      const int hpx = (args.batch * args.heads) >> 3;
+      const int i = (int)(blockIdx.x >> 3);
+      bh = (int)(blockIdx.x & 7) * hpx + i % hpx;
+      qb = args.n_qblocks - 1 - i / hpx;
+    }
   }
   const int b = bh / args.heads;
   const int h = bh - b * args.heads;

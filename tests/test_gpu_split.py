@@ -345,3 +345,21 @@ def test_xcd_table_c5r_bitwise_equals_plain_order(fa, lib, cus):
         assert p4.n_items == 0 or p4.n_merge > 0  # plain order (no table) without split
         assert torch.equal(o[:, sl], ph), f"heads {h}..{h + 3}"
         assert torch.equal(lse[:, sl], lh)
+
+
+def test_causal_head_interleave_bitwise_equals_plain_order(fa):
+    """Causal grids of several rounds with B*H divisible by 8 run each XCD's
+    heads interleaved (longest q-tiles of all its heads first).  Only the
+    order changes: outputs and LSE equal, bit for bit, those of the same
+    heads run in groups of 5, 5 and 6 (not divisible by 8: plain order)."""
+    _note("case causal head interleave")
+    q, k, v = make_qkv(1, 16, 8192, 128, "bf16", seed=case_seed(960), device=DEV)
+    o, lse = fa.forward(q, k, v, causal=True, return_lse=True, split_kv=False)
+    torch.cuda.synchronize()
+    for lo, hi in ((0, 5), (5, 10), (10, 16)):
+        sl = slice(lo, hi)
+        ph, lh = fa.forward(q[:, sl], k[:, sl], v[:, sl], causal=True, return_lse=True,
+                            split_kv=False)
+        torch.cuda.synchronize()
+        assert torch.equal(o[:, sl], ph), f"heads {lo}..{hi - 1}"
+        assert torch.equal(lse[:, sl], lh)
