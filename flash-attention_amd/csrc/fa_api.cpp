@@ -279,8 +279,9 @@ fa_status fa_fwd_plan(const fa_fwd_params* p, int32_t compute_units, fa_fwd_plan
     out->n_chunks[i] = nch;
     out->tile_begin[i] = (int32_t)((int64_t)c * T / nch);
     out->tile_end[i] = (int32_t)((int64_t)(c + 1) * T / nch);
-    out->slot[i] = nch > 1 ? a.split.slot[i] + c : -1;
-    out->head[i] = a.split.xcd_heads > 0 ? a.split.slot[i] : -1;
+    const bool table = a.split.xcd_heads > 0;
+    out->slot[i] = nch > 1 ? (table ? a.split.part[i] : a.split.slot[i]) + c : -1;
+    out->head[i] = table ? a.split.slot[i] : -1;
   }
   return FA_OK;
 }

@@ -18,11 +18,12 @@ namespace fa {
 // a second kernel.  Used when the grid would leave most of the machine idle
 // behind a few long q-tiles (short causal problems, few heads).
 //
-// XCD placement table (xcd_heads > 0, no chunks, no workspace): a causal
-// grid of one round of two workgroups per CU, where the hardware puts the
-// k-th and (k + CUs per XCD)-th workgroups of an XCD on the same CU.  The
-// table orders each XCD's q-tiles so the longest run alone and the others
-// share a CU long with short.
+// XCD placement table (xcd_heads > 0): a causal grid of one round of two
+// workgroups per CU, where the hardware puts the k-th and (k + CUs per
+// XCD)-th workgroups of an XCD on the same CU.  The table orders each XCD's
+// work items so the longest run alone and the others share a CU long with
+// short; with a workspace it may also cut the longest q-tiles in two
+// chunks (merged as in split-KV).
 constexpr int kMaxSplitItems = 128;
 
 struct SplitPlan {
@@ -39,6 +40,9 @@ struct SplitPlan {
   // Merge list: q-tile (bits 0..15) | chunk count (16..23), first slot in merge_slot.
   uint32_t merge[kMaxSplitItems];
   uint16_t merge_slot[kMaxSplitItems];
+  // XCD placement table: first partial slot of position i's q-tile (used
+  // when its chunk count is above 1).
+  uint16_t part[kMaxSplitItems];
 };
 
 struct KernelArgs {

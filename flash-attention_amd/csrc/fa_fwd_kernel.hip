@@ -561,7 +561,8 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
   if (SPLIT && n_chunks > 1) {
     // ---- split-KV partial: unnormalised O, offset m (raw score units; -inf
     // when no key of this chunk is visible to the row) and row sum l ----
-    const int64_t slot = (int64_t)args.split.slot[item] + chunk;
+    const int64_t slot =
+        (int64_t)(args.split.xcd_heads > 0 ? args.split.part[item] : args.split.slot[item]) + chunk;
     const int64_t row = ((int64_t)bh * args.split.n_slots + slot) * BM + (qrow - q0);
     if (row_ok) {
       float* po = args.ws_o + row * D;
@@ -680,8 +681,7 @@ hipError_t launch_one(const KernelArgs& a, hipStream_t stream) {
   if (sp.n_items > 0 &&
       (block_rows(args) != BM || sp.n_items > kMaxSplitItems ||
        (sp.n_merge > 0 && (args.ws_o == nullptr || args.ws_ml == nullptr)) ||
-       (sp.xcd_heads > 0 && (sp.n_merge > 0 || bh != 8 * (int64_t)sp.xcd_heads ||
-                             sp.n_items != sp.xcd_heads * args.n_qblocks))))
+       (sp.xcd_heads > 0 && bh != 8 * (int64_t)sp.xcd_heads)))
     return hipErrorInvalidValue;
   const int64_t total = sp.xcd_heads > 0 ? 8 * (int64_t)sp.n_items
                                          : (sp.n_items > 0 ? sp.n_items : args.n_qblocks) * bh;
@@ -821,39 +821,102 @@ size_t plan_chunks(const KernelArgs& a, int compute_units, SplitPlan* plan) {
 // first (the default order) pairs the longest q-tile with the (cpx+1)-th
 // longest: at B1 H16 N3000 the 47-tile q-tile shared its CU with a 32-tile
 // one and set the kernel time (66 us).  The table gives the alone
-// positions the longest q-tiles and pairs the rest longest with shortest.
-void plan_xcd_table(const KernelArgs& a, int compute_units, SplitPlan* plan) {
+// positions the longest items and pairs the rest longest with shortest.
+//
+// With allow_split the longest k q-tiles of every head may also be cut in
+// two chunks, as long as the grid stays one round (n + k * heads_per_xcd
+// <= 2 cpx); k is chosen by a model of the round: a workgroup alone costs
+// 1 per key tile, two sharing a CU 1.85 each while both run (measured
+// 1.14 us and 2.1 us per 128x64 tile), 1.5 per workgroup for its prologue,
+// and a split adds the merge (about 3.5 tile times plus the partials'
+// fp32 read-back at ~4 TB/s).  Returns the workspace bytes (0 unsplit).
+size_t plan_xcd_table(const KernelArgs& a, int compute_units, bool allow_split,
+                      SplitPlan* plan) {
   const int BM = block_rows(a);
-  if (!a.causal || BM != 128 || compute_units % 8 != 0) return;
+  if (!a.causal || BM != 128 || compute_units % 8 != 0) return 0;
   const int64_t bh = (int64_t)a.batch * a.heads;
-  if (bh % 8 != 0) return;
+  if (bh % 8 != 0) return 0;
   const int nq = (a.seq_len + BM - 1) / BM;
   const int64_t hpx = bh / 8;
   const int64_t cpx = compute_units / 8;
-  const int64_t n = hpx * nq;
-  if (n <= cpx || n > 2 * cpx || n > kMaxSplitItems) return;
-  struct Entry { int len, qb, head; };
+  const int64_t n0 = hpx * nq;
+  if (n0 <= cpx || n0 > 2 * cpx || n0 > kMaxSplitItems) return 0;
+  const int k_max =
+      allow_split ? (int)std::min<int64_t>(nq, (std::min<int64_t>(2 * cpx, kMaxSplitItems) - n0) / hpx)
+                  : 0;
+  constexpr double kShared = 2.1 / 1.14, kPrologue = 1.5, kMergeFixed = 3.5;
+  const double tile_us = a.head_dim == 128 ? 1.14 : 0.62;
+  struct Entry { int len, qb, head, c, nch; };
   Entry all[kMaxSplitItems];
-  int k = 0;
-  for (int h = 0; h < (int)hpx; ++h)
-    for (int qb = 0; qb < nq; ++qb) all[k++] = Entry{q_tile_tiles(a, BM, qb), qb, h};
-  std::stable_sort(all, all + n, [](const Entry& x, const Entry& y) {
-    return x.len != y.len ? x.len > y.len : x.qb > y.qb;
-  });
-  const int m = (int)(n - cpx);      // shared CUs
-  const int alone = (int)(cpx - m);  // CUs with one workgroup
-  // all[0, alone): alone positions [m, cpx); all[alone, n): pairs, the
-  // j-th longest of them at position j, the j-th shortest at cpx + j.
-  for (int pos = 0; pos < (int)n; ++pos) {
-    int src;
-    if (pos < m) src = alone + pos;
-    else if (pos < (int)cpx) src = pos - m;
-    else src = (int)n - 1 - (pos - (int)cpx);
-    plan->item[pos] = (uint32_t)all[src].qb | (1u << 24);  // chunk 0 of 1
-    plan->slot[pos] = (uint16_t)all[src].head;
+  auto build = [&](int k) {  // the k longest q-tiles (the last k) of every head in two chunks
+    int cnt = 0;
+    for (int h = 0; h < (int)hpx; ++h)
+      for (int qb = 0; qb < nq; ++qb) {
+        const int T = q_tile_tiles(a, BM, qb);
+        const int nch = qb >= nq - k ? 2 : 1;
+        for (int c = 0; c < nch; ++c) {
+          const int len = (int)((int64_t)(c + 1) * T / nch) - (int)((int64_t)c * T / nch);
+          all[cnt++] = Entry{len, qb, h, c, nch};
+        }
+      }
+    std::stable_sort(all, all + cnt, [](const Entry& x, const Entry& y) {
+      return x.len != y.len ? x.len > y.len : (x.qb != y.qb ? x.qb > y.qb : x.c < y.c);
+    });
+    return cnt;
+  };
+  // Position of sorted entry src for n entries: alone positions take the
+  // longest, then pairs longest-with-shortest.
+  auto position_of = [&](int n, int src) {
+    const int m = (int)(n - cpx) > 0 ? (int)(n - cpx) : 0;
+    const int alone = (int)cpx - m;
+    if (src < alone) return m + src;
+    if (src < alone + m) return src - alone;
+    return (int)cpx + (n - 1 - src);
+  };
+  auto model = [&](int k) {
+    const int n = build(k);
+    const int m = n > cpx ? n - (int)cpx : 0;
+    const int alone = (int)cpx - m;
+    double worst = 0.0;
+    for (int i = 0; i < alone && i < n; ++i) worst = std::max(worst, all[i].len + kPrologue);
+    for (int j = 0; j < m; ++j) {
+      const double x = all[alone + j].len + kPrologue, y = all[n - 1 - j].len + kPrologue;
+      worst = std::max(worst, std::min(x, y) * kShared + std::fabs(x - y));
+    }
+    if (k > 0) {
+      const double bytes = (double)bh * 2 * k * BM * ((double)a.head_dim * 4 + 8);
+      worst += kMergeFixed * 1.14 / tile_us + bytes / 4e12 / (tile_us * 1e-6);
+    }
+    return worst;
+  };
+  int best_k = 0;
+  double best = model(0);
+  for (int k = 1; k <= k_max; ++k) {
+    const double c = model(k);
+    if (c < best - 1e-9) {
+      best = c;
+      best_k = k;
+    }
   }
-  plan->n_items = (int)n;
+  const int n = build(best_k);
+  for (int src = 0; src < n; ++src) {
+    const int pos = position_of(n, src);
+    const Entry& e = all[src];
+    plan->item[pos] = (uint32_t)e.qb | ((uint32_t)e.c << 16) | ((uint32_t)e.nch << 24);
+    plan->slot[pos] = (uint16_t)e.head;
+    // partial slots: 2 per split q-tile, in q-tile order (same for every head)
+    plan->part[pos] = (uint16_t)(e.nch > 1 ? 2 * (e.qb - (nq - best_k)) : 0);
+  }
+  plan->n_items = n;
   plan->xcd_heads = (int)hpx;
+  if (best_k == 0) return 0;
+  for (int j = 0; j < best_k; ++j) {
+    plan->merge[j] = (uint32_t)(nq - best_k + j) | (2u << 16);
+    plan->merge_slot[j] = (uint16_t)(2 * j);
+  }
+  plan->n_merge = best_k;
+  plan->n_slots = 2 * best_k;
+  return (size_t)bh * plan->n_slots * BM * ((size_t)a.head_dim * 4 + 8);
 }
 
 }  // namespace
@@ -866,8 +929,7 @@ size_t plan_split(const KernelArgs& a, int compute_units, bool allow_split, Spli
     if (bytes > 0) return bytes;
     plan->n_items = plan->n_slots = plan->n_merge = 0;
   }
-  plan_xcd_table(a, compute_units, plan);
-  return 0;
+  return plan_xcd_table(a, compute_units, allow_split, plan);
 }
 
 hipError_t launch_fwd(const KernelArgs& a, hipStream_t stream) {

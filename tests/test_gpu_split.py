@@ -322,19 +322,24 @@ def test_abi_unsplit_problem_needs_no_workspace(fa, lib):
 
 
 def test_xcd_table_c5r_bitwise_equals_plain_order(fa, lib, cus):
-    """C5r runs with the XCD placement table (a dispatch order only): every
-    head's output and LSE are bit for bit those of the same heads run in
-    the plain longest-first order (4 heads per call, no table, no split)."""
+    """C5r runs with the XCD placement table.  Without a workspace
+    (split_kv=False) the table is a dispatch order only: every head's output
+    and LSE are bit for bit those of the same heads run in the plain
+    longest-first order (4 heads per call, no table, no split).  With the
+    default workspace the table also cuts the longest q-tiles in two
+    chunks: equal to the unsplit result within the split-KV bounds (its
+    rows against the oracle: test_config_sampled_rows_vs_oracle)."""
     _note("case XCD table C5r")
     q, k, v, causal, _ = make_config("C5r", device=DEV)
     pl = _plan(lib, cus, q, k, v, torch.empty_like(q), causal)
-    _note(f"  plan: xcd_heads={pl.xcd_heads} items={pl.n_items}")
+    _note(f"  plan: xcd_heads={pl.xcd_heads} items={pl.n_items} merge={pl.n_merge}")
     if cus == 256:
-        assert pl.xcd_heads == 2 and pl.n_items == 48 and pl.n_merge == 0
+        assert pl.xcd_heads == 2 and pl.n_items == 64 and pl.n_merge == 8
     o, lse = fa.forward(q, k, v, causal=True, return_lse=True)
     o2, lse2 = fa.forward(q, k, v, causal=True, return_lse=True, split_kv=False)
     torch.cuda.synchronize()
-    assert torch.equal(o, o2) and torch.equal(lse, lse2)
+    assert torch.isfinite(o).all().item()
+    _vs_unsplit(o, lse, o2, lse2, "fp16")
     for h in range(0, q.shape[1], 4):
         sl = slice(h, h + 4)
         p4 = _plan(lib, cus, q[:, sl], k[:, sl], v[:, sl], torch.empty_like(q[:, sl]), causal)
@@ -342,9 +347,8 @@ def test_xcd_table_c5r_bitwise_equals_plain_order(fa, lib, cus):
         ph, lh = fa.forward(q[:, sl], k[:, sl], v[:, sl], causal=True, return_lse=True,
                             split_kv=False)
         torch.cuda.synchronize()
-        assert p4.n_items == 0 or p4.n_merge > 0  # plain order (no table) without split
-        assert torch.equal(o[:, sl], ph), f"heads {h}..{h + 3}"
-        assert torch.equal(lse[:, sl], lh)
+        assert torch.equal(o2[:, sl], ph), f"heads {h}..{h + 3}"
+        assert torch.equal(lse2[:, sl], lh)
 
 
 def test_causal_head_interleave_bitwise_equals_plain_order(fa):

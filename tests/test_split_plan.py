@@ -37,33 +37,52 @@ def tiles(qb, N, BM, causal):
     return (kv + BN - 1) // BN
 
 
-def check_table(pl, B, H, N, causal, cus=256):
-    """XCD placement table: a permutation of one XCD's (head, q-tile) pairs
-    whose alone positions hold the longest q-tiles and whose shared CUs
-    pair long with short."""
+def check_table(pl, B, H, N, D, causal, cus=256):
+    """XCD placement table: one XCD's work items (every q-tile of its heads,
+    the longest possibly in two chunks), each key tile of each (head, q-tile)
+    exactly once; the longest items run alone and the shared CUs pair long
+    with short; chunked q-tiles have their own partial slots."""
     BM = pl.block_rows
     nq = (N + BM - 1) // BM
     hpx, cpx = B * H // 8, cus // 8
     n = pl.n_items
     assert causal and BM == 128 and B * H == 8 * pl.xcd_heads == 8 * hpx
-    assert n == hpx * nq and cpx < n <= 2 * cpx
-    assert pl.n_merge == 0 and pl.n_slots == 0 and pl.workspace_bytes == 0
-    pairs = sorted((pl.head[i], pl.q_tile[i]) for i in range(n))
-    assert pairs == [(h, q) for h in range(hpx) for q in range(nq)]
+    assert cpx < hpx * nq and n <= 2 * cpx
+    cover = {}
     for i in range(n):
-        assert pl.n_chunks[i] == 1 and pl.slot[i] == -1 and pl.tile_begin[i] == 0
-        assert pl.tile_end[i] == tiles(pl.q_tile[i], N, BM, causal)
-    lens = [pl.tile_end[i] for i in range(n)]
-    m = n - cpx
+        key = (pl.head[i], pl.q_tile[i])
+        cover.setdefault(key, []).append((pl.tile_begin[i], pl.tile_end[i], pl.n_chunks[i],
+                                          pl.slot[i]))
+    assert sorted(cover) == [(h, q) for h in range(hpx) for q in range(nq)]
+    split_q = set()
+    for (h, q), parts in cover.items():
+        parts.sort()
+        nch = parts[0][2]
+        assert len(parts) == nch and all(x[2] == nch for x in parts) and nch in (1, 2)
+        assert parts[0][0] == 0 and parts[-1][1] == tiles(q, N, BM, causal)
+        assert all(a[1] == b[0] for a, b in zip(parts, parts[1:]))
+        if nch == 1:
+            assert parts[0][3] == -1
+        else:
+            split_q.add(q)
+            assert parts[1][3] == parts[0][3] + 1
+    # the same q-tiles split in every head, the longest ones, 2 slots each
+    k = len(split_q)
+    assert split_q == set(range(nq - k, nq))
+    assert pl.n_merge == k and pl.n_slots == 2 * k
+    assert pl.workspace_bytes == B * H * 2 * k * BM * (D * 4 + 8)
+    assert n == hpx * (nq + k)
+    lens = [pl.tile_end[i] - pl.tile_begin[i] for i in range(n)]
+    m = max(n - cpx, 0)
     alone = lens[m:cpx]
     shared = [(lens[j], lens[cpx + j]) for j in range(m)]
-    if alone:
+    if alone and shared:
         assert min(alone) >= max(max(a, b) for a, b in shared)
-    # long with short: the j-th longest first occupant meets the j-th shortest second
     firsts = [a for a, _ in shared]
     seconds = [b for _, b in shared]
     assert firsts == sorted(firsts, reverse=True) and seconds == sorted(seconds)
-    assert min(firsts) >= max(seconds)
+    if shared:
+        assert min(firsts) >= max(seconds)
 
 
 def check_plan(pl, B, H, N, D, causal):
@@ -127,7 +146,7 @@ def test_baseline_configs(lib, name, B, H, N, D, causal, dtype, split):
                              (causal and dtype == A.FA_DTYPE_F16 and N >= 8192) else 128)
     if split == "table":
         assert pl.xcd_heads == 2
-        check_table(pl, B, H, N, causal)
+        check_table(pl, B, H, N, D, causal)
     elif not split:
         assert pl.n_items == 0 and pl.workspace_bytes == 0 and pl.n_slots == 0
     else:
@@ -136,28 +155,17 @@ def test_baseline_configs(lib, name, B, H, N, D, causal, dtype, split):
 
 
 def test_c5r_table_shape(lib):
-    """C5r: 2 heads x 24 q-tiles per XCD, 32 CUs: 16 shared CUs, 16 alone.
-    The 16 longest q-tiles (47, 47, 46, 46, ..., 34, 34 key tiles) run alone;
-    the 32-tile ones share with the 2-tile ones."""
+    """C5r: 2 heads x 24 q-tiles per XCD on 32 CUs, one round.  With a
+    workspace the model cuts the 8 longest q-tiles of each head (32..47 key
+    tiles) in two, which fills all 64 slots: every CU pairs its longest
+    remaining item with its shortest (32 with 2 first, chunks of 20 last).  Without the split
+    (fa_fwd) the same table has 48 items, the 16 longest alone."""
     pl = plan(lib, contiguous(B=1, H=16, N=3000, D=128, causal=1))
-    lens = [pl.tile_end[i] for i in range(pl.n_items)]
-    assert pl.n_items == 48
-    assert sorted(lens[16:32]) == sorted([47, 47] + [2 * q for q in range(17, 24) for _ in (0, 1)])
-    assert (lens[0], lens[32]) == (32, 2) and (lens[15], lens[47]) == (18, 16)
-
-
-def test_c5r_half_heads_plan_shape(lib):
-    """B1 H8 N3000 causal on 256 CUs: 24 q-tiles of 2, 4, ..., 46, 47 key
-    tiles.  Throughput bound 8*599/(256*1.1) = 17.0 tiles < 47 / 1.5 - 8:
-    split.  Average load per workgroup slot 8*599/512 = 9.4 tiles, so chunks
-    of at most S = 10 tiles: q-tiles of 12..20 tiles in 2 chunks, 22..30 in
-    3, 32..40 in 4, 42..47 in 5."""
-    pl = plan(lib, contiguous(B=1, H=8, N=3000, D=128, causal=1))
-    check_plan(pl, 1, 8, 3000, 128, 1)
-    assert pl.block_rows == 128
-    assert pl.n_merge == 19 and pl.n_slots == 5 * 2 + 5 * 3 + 5 * 4 + 4 * 5
-    assert pl.n_items == 5 + 10 + 15 + 20 + 20
-    assert max(pl.tile_end[i] - pl.tile_begin[i] for i in range(pl.n_items)) == 10
+    lens = [pl.tile_end[i] - pl.tile_begin[i] for i in range(pl.n_items)]
+    assert pl.xcd_heads == 2 and pl.n_items == 64 and pl.n_merge == 8
+    assert sorted({pl.q_tile[i] for i in range(64) if pl.n_chunks[i] == 2}) == list(range(16, 24))
+    assert (lens[0], lens[32]) == (32, 2) and (lens[31], lens[63]) == (20, 20)
+    assert max(lens) == 32
 
 
 @pytest.mark.parametrize("B,H,N,D,causal,dtype", [
@@ -190,7 +198,7 @@ def test_plan_sweep(lib, N, causal, H):
         for dtype in (A.FA_DTYPE_F16, A.FA_DTYPE_BF16):
             pl = plan(lib, contiguous(B=1, H=H, N=N, D=D, dtype=dtype, causal=causal))
             if pl.xcd_heads:
-                check_table(pl, 1, H, N, causal)
+                check_table(pl, 1, H, N, D, causal)
             elif pl.n_items:
                 check_plan(pl, 1, H, N, D, causal)
             else:
