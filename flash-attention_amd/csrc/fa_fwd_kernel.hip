@@ -30,10 +30,13 @@
 //    operand ready, and wave priorities keep the two waves of a SIMD in
 //    complementary phases (one wave's MFMAs while the other's softmax).
 //  * Causal: fully-masked K tiles are never loaded or computed; q-tiles are
-//    dispatched longest-first.  Ragged N: loads clamp to the last row and the
-//    scores of keys >= N are -inf; rows >= N are never stored.
+//    dispatched longest-first across each XCD's heads.  Ragged N: loads
+//    clamp to the last row and the scores of keys >= N are -inf; rows >= N
+//    are never stored.
 //  * Block ids are remapped so each XCD (private L2) works on consecutive
-//    q-tiles of the same heads.
+//    q-tiles of the same heads.  Causal grids of one round follow an XCD
+//    placement table instead (longest q-tiles alone on a CU, the others
+//    paired long with short; see plan_xcd_table).
 //  * Split-KV (with a caller workspace, when a few long q-tiles would set
 //    the time of a short grid): a q-tile's key tiles are cut into chunks
 //    computed by separate workgroups, which write fp32 partials (O, m, l);
