@@ -367,3 +367,50 @@ def test_causal_head_interleave_bitwise_equals_plain_order(fa):
         torch.cuda.synchronize()
         assert torch.equal(o[:, sl], ph), f"heads {lo}..{hi - 1}"
         assert torch.equal(lse[:, sl], lh)
+
+
+@pytest.mark.parametrize("B,H,N,D,dtype", [
+    (1, 16, 2200, 64, "bf16"),   # table, 11 q-tiles per head in two chunks
+    (2, 8, 3001, 128, "fp16"),   # table with chunks, ragged, two batches
+    (1, 24, 1500, 64, "fp16"),   # table over 3 heads per XCD, no chunks
+    (2, 16, 1300, 128, "bf16"),  # table over 4 heads per XCD, no chunks
+])
+def test_xcd_table_variants_vs_oracle(fa, oracle, lib, cus, B, H, N, D, dtype):
+    """XCD placement tables with and without chunks, D = 64 and 128, fp16
+    and bf16, ragged N, several heads per XCD: sampled rows against the
+    oracle and the reference-kernel emulator; the default (workspace) path
+    against split_kv=False within the split-KV bounds; and split_kv=False
+    (table order only) bit for bit against the plain order, computed one
+    batch and head at a time."""
+    _note(f"case XCD table {B}x{H}x{N}x{D} {dtype}")
+    q, k, v = make_qkv(B, H, N, D, dtype, seed=case_seed(970 + N), device=DEV)
+    pl = _plan(lib, cus, q, k, v, torch.empty_like(q), True)
+    _note(f"  plan: xcd_heads={pl.xcd_heads} items={pl.n_items} merge={pl.n_merge}")
+    if cus == 256:
+        assert pl.xcd_heads == B * H // 8
+    o, lse, o1, lse1 = _both(fa, q, k, v, True)
+    _vs_unsplit(o, lse, o1, lse1, dtype)
+    for b in range(B):
+        for h in (0, H // 2, H - 1):
+            ph, lh = fa.forward(q[b:b + 1, h:h + 1], k[b:b + 1, h:h + 1], v[b:b + 1, h:h + 1],
+                                causal=True, return_lse=True, split_kv=False)
+            torch.cuda.synchronize()
+            assert torch.equal(o1[b:b + 1, h:h + 1], ph), (b, h)
+            assert torch.equal(lse1[b:b + 1, h:h + 1], lh), (b, h)
+    rng = np.random.default_rng(970)
+    heads, sel_bh, sel_row = _sample_rows(N, B * H, rng, n_random=24)
+    qn, kn, vn = (to_np32(t.reshape(1, B * H, N, D)) for t in (q, k, v))
+    scale = 1.0 / math.sqrt(D)
+    ref_o, ref_lse = oracle.attn_rows_f64(qn, kn, vn, scale, True, sel_bh, sel_row)
+    emu_o, _ = oracle.kernel_numerics_rows(qn, kn, vn, scale, True, sel_bh, sel_row,
+                                           oracle.BF16 if dtype == "bf16" else oracle.F16)
+    got_o = to_np32(o.reshape(B * H, N, D))[sel_bh, sel_row]
+    got_lse = to_np32(lse.reshape(B * H, N))[sel_bh, sel_row]
+    mx, mean = err_stats(got_o, ref_o)
+    emx, emean = err_stats(emu_o, ref_o)
+    lse_err = float(np.abs(got_lse.astype(np.float64) - ref_lse).max())
+    _note(f"  sampled {len(sel_row)} rows: max_abs={mx:.3e} mean_abs={mean:.3e} "
+          f"(ref-kernel emu {emx:.3e}/{emean:.3e}) lse={lse_err:.3e}")
+    assert mx <= MAX_ABS_TOL
+    assert mx <= 2 * emx + 1e-6 and mean <= 2 * emean + 1e-6
+    assert lse_err <= LSE_TOL
