@@ -414,3 +414,32 @@ def test_xcd_table_variants_vs_oracle(fa, oracle, lib, cus, B, H, N, D, dtype):
     assert mx <= MAX_ABS_TOL
     assert mx <= 2 * emx + 1e-6 and mean <= 2 * emean + 1e-6
     assert lse_err <= LSE_TOL
+
+
+def test_abi_fa_fwd_table_graph_capture(fa, lib, cus):
+    """fa_fwd (no workspace) with C5r's XCD placement table, called through
+    the raw C ABI inside a captured HIP graph: every replay equals the eager
+    result, with eager launches in between."""
+    _note("case C ABI table graph capture")
+    q, k, v, causal, _ = make_config("C5r", device=DEV)
+    o = torch.empty_like(q)
+    p = A.params_from_tensors(q, k, v, o, None, causal)
+    ref = fa.forward(q, k, v, causal=True, split_kv=False)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        assert lib.fa_fwd(ctypes.byref(p), _stream()) == A.FA_OK
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    assert torch.equal(o, ref)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        assert lib.fa_fwd(ctypes.byref(p), _stream()) == A.FA_OK
+    for rep in range(3):
+        o.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(o, ref), f"replay {rep}"
+        e = fa.forward(q, k, v, causal=True)
+        torch.cuda.synchronize()
+        assert torch.isfinite(e).all().item()
