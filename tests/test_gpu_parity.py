@@ -219,6 +219,41 @@ def test_strided_bnhd_views(fa, oracle, D, causal):
     _check_against_oracle(oracle, q, k, v, o_view, lse, causal, 1.0 / math.sqrt(D), "fp16")
 
 
+@pytest.mark.parametrize("D,dtype,causal", [(128, "fp16", False), (64, "bf16", True)])
+def test_max_seq_stride_views(fa, oracle, D, dtype, causal):
+    """The largest seq stride the C ABI accepts (2^24 elements, 32 MiB between
+    rows): the K/V staging adds up to 63 rows of it to a tile's base as a
+    32-bit byte offset, and the ragged tail (N = 100) re-reads row N-1
+    through the same offsets.  Heads sit side by side inside each row (head
+    stride D).  The result must equal the contiguous one bit for bit."""
+    S = 1 << 24
+    B, H, N = 1, 2, 100
+    _note(f"case max seq stride {S} D={D} {dtype} causal={causal}")
+    q, k, v = make_qkv(B, H, N, D, dtype, seed=case_seed(81 + D), device="cpu")
+    tdt = torch.float16 if dtype == "fp16" else torch.bfloat16
+    span = (N - 1) * S + H * D
+
+    def spread(t):
+        buf = torch.empty(span, dtype=tdt, device=DEV)
+        view = buf.as_strided((B, H, N, D), (span, D, S, 1))
+        view.copy_(t.to(DEV))
+        return buf, view
+
+    (qb, qs), (kb, ks), (vb, vs), (ob, os_) = (spread(t) for t in (q, k, v, torch.zeros_like(q)))
+    try:
+        assert qs.stride(2) == S
+        out, lse = fa.forward(qs, ks, vs, os_, causal=causal, return_lse=True)
+        torch.cuda.synchronize()
+        assert out.data_ptr() == ob.data_ptr()
+        ref_o, ref_lse = _fwd(fa, q.to(DEV), k.to(DEV), v.to(DEV), causal)
+        assert torch.equal(os_, ref_o)
+        assert torch.equal(lse, ref_lse)
+        _check_against_oracle(oracle, q, k, v, os_, lse, causal, 1.0 / math.sqrt(D), dtype)
+    finally:
+        del qb, kb, vb, ob, qs, ks, vs, os_
+        torch.cuda.empty_cache()
+
+
 def test_config_c1_full_vs_oracle(fa, oracle):
     """C1 (the reference's CPU-runnable case) end to end, every row."""
     q, k, v, causal, scale = make_config("C1")
