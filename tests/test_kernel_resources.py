@@ -1,0 +1,83 @@
+"""Build properties of the gfx950 forward kernels, read from the device
+assembly that hipcc emits for csrc/fa_fwd_kernel.hip with the library's own
+flags (CPU only: hipcc cross-compiles without a GPU).
+
+- Every forward variant fits two waves per SIMD (at most 256 VGPRs, no
+  AGPRs), with no scratch and no VGPR spills.
+- m0 discipline of the K/V staging: the DMA is issued from inline asm that
+  sets m0 (the LDS destination) immediately before each
+  global_load_lds_dwordx4 and declares m0 clobbered.  The compiler does not
+  save a reserved register around such an asm, so the kernels must not use
+  m0 for anything else: every m0 reference in the assembly is one of those
+  writes, and each is followed by its DMA instruction.
+"""
+from __future__ import annotations
+
+import os
+import re
+import shutil
+import subprocess
+import sys
+
+import pytest
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+sys.path.insert(0, os.path.join(REPO, "flash-attention_amd"))
+
+
+@pytest.fixture(scope="module")
+def device_asm(tmp_path_factory):
+    import build as fa_build  # flash-attention_amd/build.py
+
+    try:
+        hipcc = fa_build._hipcc()
+    except RuntimeError:
+        pytest.skip("hipcc not available")
+    out = str(tmp_path_factory.mktemp("asm") / "fa_fwd_kernel.s")
+    flags = [f for f in fa_build.HIP_FLAGS if f not in ("-fPIC", "-Wall")]
+    cmd = [hipcc, *flags, "-I", fa_build.INCLUDE, "-I", fa_build.CSRC, "-x", "hip",
+           "--cuda-device-only", "-S", os.path.join(fa_build.CSRC, "fa_fwd_kernel.hip"),
+           "-o", out]
+    proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    assert proc.returncode == 0, proc.stdout[-4000:]
+    with open(out) as f:
+        return f.read()
+
+
+def _kernel_metadata(asm: str):
+    """(name, {field: value}) per kernel from the amdhsa.kernels metadata."""
+    meta = asm[asm.index("amdhsa.kernels:"):]
+    kernels = []
+    for block in re.split(r"\n  - ", meta)[1:]:
+        fields = dict(re.findall(r"^    \.(\w+):\s+(\S+)$", block, re.M))
+        if "name" in fields:
+            kernels.append((fields["name"], fields))
+    return kernels
+
+
+def test_forward_variants_fit_two_waves_per_simd(device_asm):
+    kernels = _kernel_metadata(device_asm)
+    fwd = [(n, f) for n, f in kernels if "fa_fwd_kernel" in n]
+    assert len(fwd) == 28, [n for n, _ in kernels]
+    assert sum("fa_merge_kernel" in n for n, _ in kernels) == 4
+    for name, f in kernels:
+        assert int(f["private_segment_fixed_size"]) == 0, (name, "scratch")
+        assert int(f["vgpr_spill_count"]) == 0, (name, "VGPR spills")
+        assert int(f.get("agpr_count", "0")) == 0, (name, "AGPRs")
+        assert int(f["vgpr_count"]) <= 256, (name, f["vgpr_count"])
+    for name, f in fwd:
+        # K/V ring: 4 tiles of 64 keys x D fp16 (+ the optimistic pass's flag).
+        d = 128 if "Li128E" in name else 64
+        assert int(f["group_segment_fixed_size"]) in (4 * 64 * 2 * d, 4 * 64 * 2 * d + 4), name
+
+
+def test_m0_only_set_for_the_staging_dma(device_asm):
+    lines = [ln.strip() for ln in device_asm.splitlines()]
+    code = [ln for ln in lines if ln and not ln.startswith(";") and not ln.startswith(".")]
+    m0_refs = [i for i, ln in enumerate(code) if re.search(r"\bm0\b", ln)]
+    dma = [i for i, ln in enumerate(code) if ln.startswith("global_load_lds_dwordx4")]
+    assert dma, "no staging DMA found"
+    assert len(m0_refs) == len(dma)
+    for i in m0_refs:
+        assert re.fullmatch(r"s_mov_b32 m0, s\d+", code[i]), code[i]
+        assert code[i + 1].startswith("global_load_lds_dwordx4"), (code[i], code[i + 1])
