@@ -200,7 +200,10 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // the s_waitcnt, which are side-effecting too), and each tile ends with
 // s_waitcnt vmcnt(0) followed by a workgroup barrier before any wave reads
 // the freshly written buffer; a buffer is refilled only after the barrier
-// that ends the tile which last read it.
+// that ends the tile which last read it.  m0 (the LDS destination) is set
+// inside the asm and declared clobbered; the compiler does not preserve a
+// reserved register around inline asm, so nothing else in these kernels may
+// use m0 (tests/test_kernel_resources.py checks the emitted assembly).
 __device__ __forceinline__ void dma_16b(uint32_t voff, const char* sbase, uint32_t lds_base) {
   asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
                :
