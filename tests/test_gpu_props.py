@@ -10,7 +10,9 @@ the fp64 oracle cannot cover every row:
     unchanged;
   * V constant: every O row is a convex combination of the V rows, so O == c;
   * a captured HIP graph replays to the eager result, several times, with
-    eager work in between.
+    eager work in between;
+  * the entry points are re-entrant across streams and host threads, with a
+    per-thread last-error message.
 """
 from __future__ import annotations
 
@@ -118,4 +120,64 @@ def test_concurrent_streams_match_sequential(fa):
             fa.forward(q, k, v, o, causal=c)
     torch.cuda.synchronize()
     for o, r in zip(outs, ref):
+        assert torch.equal(o, r)
+
+
+def test_host_threads_share_the_library(fa):
+    """The C ABI called from four host threads at once (ctypes releases the
+    GIL), each on its own stream with its own workspace: the results equal
+    the single-threaded ones, and each thread's fa_last_error() is its own (a
+    rejected call's message survives the other threads' calls, which clear
+    and set theirs meanwhile)."""
+    import ctypes
+    import threading
+
+    import abi_ctypes as A
+
+    _note("case host threads")
+    L = A.load()
+    probs = [make_config(n, device=DEV) for n in ("C2", "C5r", "C2", "C5r")]
+    refs = [fa.forward(q, k, v, causal=c) for q, k, v, c, _ in probs]
+    outs = [torch.empty_like(p[0]) for p in probs]
+    streams = [torch.cuda.Stream() for _ in probs]
+    params, wss = [], []
+    for (q, k, v, c, _), o in zip(probs, outs):
+        p = A.params_from_tensors(q, k, v, o, causal=c)
+        need = ctypes.c_uint64(0)
+        assert L.fa_fwd_workspace_size(ctypes.byref(p), ctypes.byref(need)) == A.FA_OK
+        params.append(p)
+        wss.append((torch.empty(max(int(need.value), 16), dtype=torch.uint8, device=DEV),
+                    int(need.value)))
+    torch.cuda.synchronize()
+    errors = []
+
+    def work(i):
+        try:
+            p, (ws, nbytes), st = params[i], wss[i], streams[i].cuda_stream
+            bad = A.FaFwdParams.from_buffer_copy(p)
+            bad.head_dim = 96
+            for it in range(20):
+                rc = L.fa_fwd_ws(ctypes.byref(p), ctypes.c_void_p(ws.data_ptr()), nbytes,
+                                 ctypes.c_void_p(st))
+                if rc != A.FA_OK:
+                    errors.append((i, it, rc, L.fa_last_error()))
+                    return
+                if L.fa_fwd(ctypes.byref(bad), ctypes.c_void_p(st)) != A.FA_ERR_HEADDIM:
+                    errors.append((i, it, "head_dim 96 accepted"))
+                    return
+                msg = L.fa_last_error().decode()
+                if "head_dim" not in msg or "96" not in msg:
+                    errors.append((i, it, msg))
+                    return
+        except Exception as e:  # reported below, in the test's thread
+            errors.append((i, repr(e)))
+
+    threads = [threading.Thread(target=work, args=(i,)) for i in range(len(probs))]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    torch.cuda.synchronize()
+    assert not errors, errors
+    for o, r in zip(outs, refs):
         assert torch.equal(o, r)
