@@ -168,7 +168,9 @@ fa_status fa_fwd_plan(const fa_fwd_params* p, int32_t compute_units, fa_fwd_plan
 /* Static description of a status code. */
 const char* fa_status_str(fa_status s);
 
-/* Detail of the last failure on the calling thread ("" if none). */
+/* Detail of the last failure on the calling thread ("" if none).  The string
+ * belongs to the library (thread-local storage) and stays valid until the
+ * same thread's next call into the library. */
 const char* fa_last_error(void);
 
 /* Query device `device`.  Returns FA_OK, FA_ERR_NULL or FA_ERR_HIP. */
