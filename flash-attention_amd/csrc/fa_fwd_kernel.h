@@ -64,7 +64,7 @@ struct KernelArgs {
   float scale_log2;   // softmax scale * log2(e), used for exp2
   // Split-KV (filled by the launcher when a workspace is used).
   float* ws_o;        // [batch*heads][n_slots][BM][head_dim] fp32 partial O
-  float* ws_ml;       // [batch*heads][n_slots][BM][2] fp32 (m, l)
+  float* ws_ml;       // [batch*heads][n_slots][BM][4] fp32 (m, l, lr, unused)
   SplitPlan split;
 };
 

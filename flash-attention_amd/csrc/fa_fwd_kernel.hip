@@ -52,11 +52,13 @@
 // reach 2^15 (the common factor exp2(m_max*c - m*c) cancels in O/l), so the
 // row max is computed only on such tiles (fp16 non-causal and fp16 causal in
 // 8-wave workgroups run an optimistic pass with the offset of the first tile
-// and redo the workgroup with per-tile checks only if a P overflowed); l is
-// the sum of the rounded P (the weights P V actually uses) in the optimistic
-// pass and in the checked pass of fp16 at D = 128, and of the unrounded p,
-// as the reference, in the checked pass of bf16 and of fp16 at D = 64; and
-// the natural-log LSE = m*scale + ln(l) is new.
+// and redo the workgroup with per-tile checks only if a P overflowed); O is
+// normalised by the sum of the rounded P (the weights P V actually uses: with
+// the lazy offset the largest P of a row is not exactly 1, and this makes its
+// rounding cancel); the LSE uses the sum of the unrounded p, as the
+// reference's l, in the checked pass of bf16 and of fp16 at D = 64, and the
+// rounded sum elsewhere (fp16, relative error <= 2^-11 per term); and the
+// natural-log LSE = m*scale + ln(l) is new.
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -150,10 +152,16 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
   constexpr int KSTEPS = D / 16;  // MFMA k-steps for S^T (k = head dim)
   constexpr int DBLK = D / 32;    // 32-wide head-dim blocks of O^T
   constexpr int ITERS = T::BYTES / (1024 * NW);  // DMA instructions per wave per tile
-  // Row sums of P in the per-tile checked pass: fp32 sums of the unrounded p
-  // for bf16, and for fp16 at D = 64, where the softmax is twice as dense per
-  // MFMA and two v_add_f32 issue faster than one v_dot2c_f32_f16 (+8 % at
-  // B4 H16 N1024 D64); fp16 at D = 128 sums the rounded P with v_dot2c.
+  // Row sums of P in the per-tile checked pass.  O is always normalised by
+  // the sum of the rounded P (the weights P V actually uses, so the weights
+  // of a row sum to 1 and a dominant key's rounding cancels; with a lazy
+  // offset the largest P of a row is not exactly 1 as in the reference).
+  // bf16, and fp16 at D = 64, also keep fp32 sums of the unrounded p for the
+  // tile check and the LSE, as the reference's l (online_softmax.cuh:135-152):
+  // bf16's 8 significant bits would cost up to 2^-9 in the LSE, and at D = 64
+  // the softmax is twice as dense per MFMA, where two v_add_f32 issue faster
+  // than one v_dot2c_f32_f16 for the check (+8 % at B4 H16 N1024 D64).  fp16
+  // at D = 128 uses the rounded sum (v_dot2c) for all three.
   constexpr bool kUnroundedSum = BF16 || D == 64;
   // fp16, 8-wave or non-causal: the row sums of the rounded P run on the
   // matrix core (row_sum_mfma, 4 small MFMAs per tile in place of 16 v_dot2c
@@ -311,7 +319,8 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
   const float c = args.scale_log2;
   float m_run = -INFINITY;  // offset used in the exponent (<= the running max)
   float neg_mc = INFINITY;  // -m_run * c; +inf while m_run = -inf (trips the first check)
-  float l_run = 0.0f;       // this lane's partial sum of P
+  float l_run = 0.0f;       // this lane's partial sum of P (unrounded p when kUnroundedSum)
+  float lr_run = 0.0f;      // kUnroundedSum: this lane's partial sum of the rounded P
   f32x4 l_mfma = {0.0f, 0.0f, 0.0f, 0.0f};  // row sums on the matrix core (kMfmaSums)
   const f16x8 sum_sel = row_sum_selector(lane);
 
@@ -409,10 +418,11 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
     // P is packed as the P^T B operand: chunk ch = 2kb + hh uses S registers
     // 8hh..8hh+7 of block kb.  t0/t1 sum this lane's even/odd keys.
     i16x8 pf[4];
-    float t0, t1;
+    float t0, t1, tr;
     auto exp_pack = [&](float nmc) FA_INLINE {
       t0 = 0.0f;
       t1 = 0.0f;
+      tr = 0.0f;
 #pragma unroll
       for (int ch = 0; ch < 4; ++ch) {
         const int kb = ch >> 1, base = (ch & 1) * 8;
@@ -424,10 +434,11 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
           w[j] = pack2<BF16>(p0, p1);
           if constexpr (kUnroundedSum && !OPT) {
             // Sum the unrounded fp32 p, as the reference does
-            // (online_softmax.cuh:135-152).  bf16 needs it: its 8
-            // significant bits would cost up to 2^-9 in the LSE.
+            // (online_softmax.cuh:135-152), for the check and the LSE, and
+            // the rounded P for the normalisation.
             t0 += p0;
             t1 += p1;
+            tr = dot2_acc<BF16>(w[j], tr);
           }
         }
         pf[ch] = __builtin_bit_cast(i16x8, w);
@@ -480,6 +491,7 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
       const float alpha = fast_exp2(grow ? (m_run - m_new) * c : 0.0f);
       m_run = m_new;
       l_run *= alpha;
+      if constexpr (kUnroundedSum) lr_run *= alpha;
 #pragma unroll
       for (int db = 0; db < DBLK; ++db)
 #pragma unroll
@@ -490,7 +502,10 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
       neg_mc = none ? INFINITY : -m_run * c;
       exp_pack(none ? 0.0f : neg_mc);
     }
-    if constexpr (!OPT) l_run += t0 + t1;
+    if constexpr (!OPT) {
+      l_run += t0 + t1;
+      if constexpr (kUnroundedSum) lr_run += tr;
+    }
 
     // ---- O^T += V^T P^T ----
     // 4-wave workgroups: raised wave priority while this wave issues its PV
@@ -532,7 +547,9 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
       if (t + 1 < t_end) tile_step(std::integral_constant<int, 1>{}, t + 1, opt_c);
     }
   };
-  float l_tot;
+  // l_tot: the row sum for the LSE; lr_tot: the sum of the rounded P, which
+  // normalises O (the same value unless kUnroundedSum).
+  float l_tot, lr_tot;
   if constexpr (kMfmaSums) {
     run_tiles(std::true_type{});
     l_tot = row_sum_of_lane(l_mfma, lane);
@@ -541,6 +558,7 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
     // done with the K/V ring.
     if (__any(!(l_tot < INFINITY)) && lane == 0) redo_flag = 1;
     __syncthreads();
+    lr_tot = l_tot;
     if (redo_flag != 0) {
 #pragma unroll
       for (int db = 0; db < DBLK; ++db)
@@ -549,21 +567,25 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
       m_run = -INFINITY;
       neg_mc = INFINITY;
       l_run = 0.0f;
+      lr_run = 0.0f;
       issue_tile(t_begin, 0);
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
       run_tiles(std::false_type{});
       l_tot = pair_sum(l_run);
+      lr_tot = kUnroundedSum ? pair_sum(lr_run) : l_tot;
     }
   } else {
     run_tiles(std::false_type{});
     l_tot = pair_sum(l_run);
+    lr_tot = kUnroundedSum ? pair_sum(lr_run) : l_tot;
   }
 
   const bool row_ok = qrow < N;
   if (SPLIT && n_chunks > 1) {
     // ---- split-KV partial: unnormalised O, offset m (raw score units; -inf
-    // when no key of this chunk is visible to the row) and row sum l ----
+    // when no key of this chunk is visible to the row), the row sum l for the
+    // LSE and the sum of the rounded P for the normalisation ----
     const int64_t slot =
         (int64_t)(args.split.xcd_heads > 0 ? args.split.part[item] : args.split.slot[item]) + chunk;
     const int64_t row = ((int64_t)bh * args.split.n_slots + slot) * BM + (qrow - q0);
@@ -578,13 +600,14 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
                            o_acc[db][4 * r + 3]};
           *reinterpret_cast<f32x4*>(po + col) = w;
         }
-      if (g == 0) *reinterpret_cast<f32x2*>(args.ws_ml + row * 2) = f32x2{m_run, l_tot};
+      if (g == 0)
+        *reinterpret_cast<f32x4*>(args.ws_ml + row * 4) = f32x4{m_run, l_tot, lr_tot, 0.0f};
     }
     return;
   }
 
   // ---- epilogue: normalise, store ----
-  const float inv_l = (row_ok && l_tot > 0.0f) ? 1.0f / l_tot : 0.0f;
+  const float inv_l = (row_ok && lr_tot > 0.0f) ? 1.0f / lr_tot : 0.0f;
   if (row_ok) {
     char* op = oh + qrow * osb;
 #pragma unroll
@@ -604,10 +627,11 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
 }
 
 // Split-KV merge: one thread per 4 head-dim elements of a row of a q-tile
-// with more than one chunk.  O = sum_c w_c O_c / sum_c w_c l_c with
+// with more than one chunk.  O = sum_c w_c O_c / sum_c w_c lr_c with
 // w_c = exp2((m_c - m) * c) and m = max_c m_c (the single-pass online
-// softmax regrouped by chunk; chunks whose rows saw no key have l_c = 0 and
-// are skipped), LSE = m * scale + ln(l).  Chunks are read kMergeGroup at a
+// softmax regrouped by chunk; lr_c is chunk c's sum of the rounded P, and
+// chunks whose rows saw no key have l_c = 0 and are skipped),
+// LSE = m * scale + ln(sum_c w_c l_c).  Chunks are read kMergeGroup at a
 // time with all loads issued together, so a row costs one memory latency
 // per group rather than one per chunk.
 constexpr int kMergeGroup = 4;
@@ -632,15 +656,15 @@ __global__ void __launch_bounds__(256) fa_merge_kernel(const KernelArgs args, in
   // was visible), so every load below reads written data.
   const int64_t row0 = ((int64_t)bh * args.split.n_slots + args.split.merge_slot[mi]) * BM + r;
   const float c2 = args.scale_log2;
-  float m = -INFINITY, l = 0.0f;
+  float m = -INFINITY, l = 0.0f, lr = 0.0f;
   f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
   for (int c0 = 0; c0 < nch; c0 += kMergeGroup) {
-    f32x2 ml[kMergeGroup];
+    f32x4 ml[kMergeGroup];  // (m, l, lr, unused)
     f32x4 oc[kMergeGroup];
 #pragma unroll
     for (int j = 0; j < kMergeGroup; ++j) {
       const int64_t rc = row0 + (int64_t)min(c0 + j, nch - 1) * BM;
-      ml[j] = *reinterpret_cast<const f32x2*>(args.ws_ml + rc * 2);
+      ml[j] = *reinterpret_cast<const f32x4*>(args.ws_ml + rc * 4);
       oc[j] = *reinterpret_cast<const f32x4*>(args.ws_o + rc * D + d);
     }
     float mg = m;
@@ -650,6 +674,7 @@ __global__ void __launch_bounds__(256) fa_merge_kernel(const KernelArgs args, in
     if (l > 0.0f && mg > m) {
       const float a = fast_exp2((m - mg) * c2);
       l *= a;
+      lr *= a;
       acc *= a;
     }
     m = mg;
@@ -658,10 +683,11 @@ __global__ void __launch_bounds__(256) fa_merge_kernel(const KernelArgs args, in
       if (c0 + j < nch && ml[j][1] > 0.0f) {
         const float w = fast_exp2((ml[j][0] - m) * c2);
         l += w * ml[j][1];
+        lr += w * ml[j][2];
         acc += w * oc[j];
       }
   }
-  const float inv_l = l > 0.0f ? 1.0f / l : 0.0f;
+  const float inv_l = lr > 0.0f ? 1.0f / lr : 0.0f;
   const int b = bh / args.heads;
   const int h = bh - b * args.heads;
   char* op = reinterpret_cast<char*>(args.o) +
@@ -689,21 +715,24 @@ hipError_t launch_one(const KernelArgs& a, hipStream_t stream) {
   const int64_t total = sp.xcd_heads > 0 ? 8 * (int64_t)sp.n_items
                                          : (sp.n_items > 0 ? sp.n_items : args.n_qblocks) * bh;
   if (total > 0x7fffffff) return hipErrorInvalidValue;
-  if (args.split.n_items == 0) {
-    hipLaunchKernelGGL((fa_fwd_kernel<D, BF16, CAUSAL, NW, false>), dim3((unsigned)total),
-                       dim3(NW * 64), 0, stream, args);
-    return hipGetLastError();
-  }
-  hipLaunchKernelGGL((fa_fwd_kernel<D, BF16, CAUSAL, NW, true>), dim3((unsigned)total),
-                     dim3(NW * 64), 0, stream, args);
-  hipError_t e = hipGetLastError();
+  // hipLaunchKernel returns this launch's own status: the thread's last-error
+  // state is neither read nor cleared, so an earlier failure of an unrelated
+  // HIP call by the caller is not reported as (or lost to) this launch.
+  void* kargs[] = {&args};
+  if (args.split.n_items == 0)
+    return hipLaunchKernel(reinterpret_cast<const void*>(&fa_fwd_kernel<D, BF16, CAUSAL, NW, false>),
+                           dim3((unsigned)total), dim3(NW * 64), kargs, 0, stream);
+  hipError_t e =
+      hipLaunchKernel(reinterpret_cast<const void*>(&fa_fwd_kernel<D, BF16, CAUSAL, NW, true>),
+                      dim3((unsigned)total), dim3(NW * 64), kargs, 0, stream);
   if (e != hipSuccess || sp.n_merge == 0) return e;
   constexpr int RPB = 256 / (D / 4);
   const int64_t merge_blocks = bh * args.split.n_merge * ((BM + RPB - 1) / RPB);
   if (merge_blocks > 0x7fffffff) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((fa_merge_kernel<D, BF16>), dim3((unsigned)merge_blocks), dim3(256), 0,
-                     stream, args, BM);
-  return hipGetLastError();
+  int bm = BM;
+  void* margs[] = {&args, &bm};
+  return hipLaunchKernel(reinterpret_cast<const void*>(&fa_merge_kernel<D, BF16>),
+                         dim3((unsigned)merge_blocks), dim3(256), margs, 0, stream);
 }
 
 template <int D, bool BF16>
@@ -812,8 +841,8 @@ size_t plan_chunks(const KernelArgs& a, int compute_units, SplitPlan* plan) {
   plan->n_items = n;
   plan->n_slots = n_slots;
   plan->n_merge = n_merge;
-  // Partial O (fp32) then (m, l) per row of every slot.
-  return (size_t)a.batch * a.heads * n_slots * BM * ((size_t)a.head_dim * 4 + 8);
+  // Partial O (fp32) then (m, l, lr, unused) per row of every slot.
+  return (size_t)a.batch * a.heads * n_slots * BM * ((size_t)a.head_dim * 4 + 16);
 }
 
 // XCD placement table for a causal 4-wave grid of one round: each XCD
@@ -887,7 +916,7 @@ size_t plan_xcd_table(const KernelArgs& a, int compute_units, bool allow_split,
       worst = std::max(worst, std::min(x, y) * kShared + std::fabs(x - y));
     }
     if (k > 0) {
-      const double bytes = (double)bh * 2 * k * BM * ((double)a.head_dim * 4 + 8);
+      const double bytes = (double)bh * 2 * k * BM * ((double)a.head_dim * 4 + 16);
       worst += kMergeFixed * 1.14 / tile_us + bytes / 4e12 / (tile_us * 1e-6);
     }
     return worst;
@@ -919,7 +948,7 @@ size_t plan_xcd_table(const KernelArgs& a, int compute_units, bool allow_split,
   }
   plan->n_merge = best_k;
   plan->n_slots = 2 * best_k;
-  return (size_t)bh * plan->n_slots * BM * ((size_t)a.head_dim * 4 + 8);
+  return (size_t)bh * plan->n_slots * BM * ((size_t)a.head_dim * 4 + 16);
 }
 
 }  // namespace

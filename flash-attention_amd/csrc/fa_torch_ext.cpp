@@ -3,11 +3,12 @@
 // Mirrors the reference's pybind extension python/flash_attention_runtime/
 // _ext.cu (check_cuda_tensor / validate_inputs :19-57, launch_fp16 :59-122,
 // fa_forward :124-158, PYBIND11_MODULE :162-173): same positional signature
-// forward(q, k, v, o=None, benchmark=False) -> (o, ms), the same validation
-// messages where the rule is the same, output allocated with empty_like(q)
-// when o is not given, launch on the current stream.  It adds keyword
-// arguments causal, softmax_scale, return_lse and split_kv, and accepts bf16,
-// head_dim 64, any seq_len >= 1 and strided [B,H,N,D] views with unit
+// and result, forward(q, k, v, o=None, benchmark=False) -> (o, ms) with ms
+// = 0 unless benchmark, the same validation messages where the rule is the
+// same, output allocated with empty_like(q) when o is not given, launch on
+// the current stream.  It adds keyword-only arguments causal, softmax_scale,
+// return_lse (then the result is (o, ms, lse)) and split_kv, and accepts
+// bf16, head_dim 64, any seq_len >= 1 and strided [B,H,N,D] views with unit
 // head_dim stride.  With split_kv the split-KV workspace comes from torch's
 // caching allocator on the current stream.
 //
@@ -20,7 +21,6 @@
 
 #include <cmath>
 #include <optional>
-#include <tuple>
 
 #include "fa_mi355x.h"
 
@@ -80,7 +80,9 @@ fa_fwd_params make_params(const torch::Tensor& q, const torch::Tensor& k, const 
   return p;
 }
 
-std::tuple<torch::Tensor, double, std::optional<torch::Tensor>> fa_forward(
+// Returns (o, ms), or (o, ms, lse) with return_lse: the reference's callers
+// index and unpack the pair (python/flash_attention_runtime/__init__.py:31,37).
+pybind11::tuple fa_forward(
     const torch::Tensor& q, const torch::Tensor& k, const torch::Tensor& v,
     std::optional<torch::Tensor> o_opt, bool benchmark, bool causal,
     std::optional<double> softmax_scale, bool return_lse, bool split_kv) {
@@ -119,7 +121,8 @@ std::tuple<torch::Tensor, double, std::optional<torch::Tensor>> fa_forward(
     s = benchmark ? fa_fwd_timed(&p, stream, &ms) : fa_fwd(&p, stream);
   TORCH_CHECK(s == FA_OK, "flash attention forward failed: ", fa_status_str(s), ": ",
               fa_last_error());
-  return {o, static_cast<double>(ms), lse};
+  if (return_lse) return pybind11::make_tuple(o, static_cast<double>(ms), *lse);
+  return pybind11::make_tuple(o, static_cast<double>(ms));
 }
 
 pybind11::dict device_info(int device) {
@@ -145,6 +148,7 @@ pybind11::dict device_info(int device) {
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("forward", &fa_forward, pybind11::arg("q"), pybind11::arg("k"), pybind11::arg("v"),
         pybind11::arg("o") = std::optional<torch::Tensor>{}, pybind11::arg("benchmark") = false,
+        pybind11::kw_only(),
         pybind11::arg("causal") = false, pybind11::arg("softmax_scale") = std::optional<double>{},
         pybind11::arg("return_lse") = false, pybind11::arg("split_kv") = true,
         "FlashAttention-2 forward (MI355X / gfx950, HIP)");

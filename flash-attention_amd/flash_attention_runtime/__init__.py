@@ -58,8 +58,9 @@ def forward(
 
     Returns ``o`` (same dtype as q), or ``(o, lse)`` when ``return_lse``.
     """
-    out, _ms, lse = _EXT.forward(q, k, v, o, False, causal, softmax_scale, return_lse, split_kv)
-    return (out, lse) if return_lse else out
+    res = _EXT.forward(q, k, v, o, False, causal=causal, softmax_scale=softmax_scale,
+                       return_lse=return_lse, split_kv=split_kv)
+    return (res[0], res[2]) if return_lse else res[0]
 
 
 def forward_timed(
@@ -78,8 +79,8 @@ def forward_timed(
 
     Returns ``(o, ms)``, or ``(o, ms, lse)`` when ``return_lse``.
     """
-    out, ms, lse = _EXT.forward(q, k, v, o, True, causal, softmax_scale, return_lse, split_kv)
-    return (out, ms, lse) if return_lse else (out, ms)
+    return tuple(_EXT.forward(q, k, v, o, True, causal=causal, softmax_scale=softmax_scale,
+                              return_lse=return_lse, split_kv=split_kv))
 
 
 def device_info(device: int = 0) -> dict:

@@ -56,6 +56,7 @@
  */
 #include "attn_oracle.h"
 
+#include <immintrin.h>
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
@@ -159,7 +160,7 @@ static void row_f64(const float* q, const float* k, const float* v, int N, int D
     const float* qr = q + (int64_t)((mutation == ORACLE_MUT_TRANSPOSE_S) ? j : i) * D;
     const float* kr = k + (int64_t)((mutation == ORACLE_MUT_TRANSPOSE_S) ? i : j) * D;
     double acc = 0.0;
-    for (int d = 0; d < D; ++d) acc += (double)qr[d] * (double)kr[d];
+    for (int d = 0; d < D; ++d) acc = fma((double)qr[d], (double)kr[d], acc);
     s[j] = sc * acc;
     if (s[j] > m) m = s[j];
   }
@@ -173,7 +174,7 @@ static void row_f64(const float* q, const float* k, const float* v, int N, int D
     const double p = exp(s[j] - m);
     l += p;
     const float* vr = v + (int64_t)j * D;
-    for (int d = 0; d < D; ++d) o_row[d] += p * (double)vr[d];
+    for (int d = 0; d < D; ++d) o_row[d] = fma(p, (double)vr[d], o_row[d]);
   }
   if (mutation != ORACLE_MUT_NO_NORMALISE)
     for (int d = 0; d < D; ++d) o_row[d] /= l;
@@ -206,26 +207,138 @@ int oracle_attn_rows_f64(const float* q, const float* k, const float* v, int B, 
   return err;
 }
 
+/* Rows [i0, i0 + nr) of one head at once (nr <= ORACLE_RB), mutation 0.
+ * A single row's dot product is one dependent chain of D fused
+ * multiply-adds, which leaves the FMA units mostly idle; a block of rows
+ * against the same key gives ORACLE_RB independent chains.  Each row keeps
+ * row_f64's arithmetic exactly (dot over d ascending, max, exp, l and O
+ * summed over j ascending, all with explicit fma), so every output equals
+ * row_f64's bit for bit (tests/test_oracle.py checks this).
+ * Scratch: qt holds D x ORACLE_RB doubles, s ORACLE_RB x N. */
+#define ORACLE_RB 16
+static void rows_block_f64(const float* q, const float* k, const float* v, int N, int D,
+                           double scale, int causal, int i0, int nr, double* qt, double* s,
+                           double* o_rows, double* lse_rows) {
+  for (int d = 0; d < D; ++d)
+    for (int r = 0; r < ORACLE_RB; ++r)
+      qt[d * ORACLE_RB + r] = r < nr ? (double)q[(int64_t)(i0 + r) * D + d] : 0.0;
+  /* keys [0, jend) are visible to some row of the block */
+  const int jend = causal ? (i0 + nr < N ? i0 + nr : N) : N;
+  int j = 0;
+  /* two keys x 16 rows: 8 independent 4-wide fma chains */
+  for (; j + 1 < jend; j += 2) {
+    const float* k0 = k + (int64_t)j * D;
+    const float* k1 = k0 + D;
+    __m256d a[2][4];
+    for (int u = 0; u < 4; ++u) a[0][u] = a[1][u] = _mm256_setzero_pd();
+    for (int d = 0; d < D; ++d) {
+      const __m256d x0 = _mm256_set1_pd((double)k0[d]), x1 = _mm256_set1_pd((double)k1[d]);
+      const double* qd = qt + d * ORACLE_RB;
+      for (int u = 0; u < 4; ++u) {
+        const __m256d qv = _mm256_loadu_pd(qd + 4 * u);
+        a[0][u] = _mm256_fmadd_pd(qv, x0, a[0][u]);
+        a[1][u] = _mm256_fmadd_pd(qv, x1, a[1][u]);
+      }
+    }
+    double a0[ORACLE_RB], a1[ORACLE_RB];
+    for (int u = 0; u < 4; ++u) {
+      _mm256_storeu_pd(a0 + 4 * u, a[0][u]);
+      _mm256_storeu_pd(a1 + 4 * u, a[1][u]);
+    }
+    for (int r = 0; r < ORACLE_RB; ++r) {
+      s[(int64_t)r * N + j] = scale * a0[r];
+      s[(int64_t)r * N + j + 1] = scale * a1[r];
+    }
+  }
+  for (; j < jend; ++j) {
+    const float* k0 = k + (int64_t)j * D;
+    double a0[ORACLE_RB];
+    for (int r = 0; r < ORACLE_RB; ++r) a0[r] = 0.0;
+    for (int d = 0; d < D; ++d) {
+      const double x0 = (double)k0[d];
+      const double* qd = qt + d * ORACLE_RB;
+      for (int r = 0; r < ORACLE_RB; ++r) a0[r] = fma(qd[r], x0, a0[r]);
+    }
+    for (int r = 0; r < ORACLE_RB; ++r) s[(int64_t)r * N + j] = scale * a0[r];
+  }
+  double l[ORACLE_RB];
+  int jmax[ORACLE_RB];
+  for (int r = 0; r < nr; ++r) {
+    double* sr = s + (int64_t)r * N;
+    jmax[r] = causal ? i0 + r + 1 : N;
+    double m = -INFINITY;
+    for (int jj = 0; jj < jmax[r]; ++jj)
+      if (sr[jj] > m) m = sr[jj];
+    double lr = 0.0;
+    for (int jj = 0; jj < jmax[r]; ++jj) {
+      sr[jj] = exp(sr[jj] - m); /* p_j, in place */
+      lr += sr[jj];
+    }
+    l[r] = lr;
+    lse_rows[r] = m + log(lr);
+    for (int d = 0; d < D; ++d) o_rows[(int64_t)r * D + d] = 0.0;
+  }
+  for (int jj = 0; jj < jend; ++jj) {
+    const float* vr = v + (int64_t)jj * D;
+    for (int r = 0; r < nr; ++r) {
+      if (jj >= jmax[r]) continue;
+      const double p = s[(int64_t)r * N + jj];
+      double* orow = o_rows + (int64_t)r * D;
+      for (int d = 0; d < D; ++d) orow[d] = fma(p, (double)vr[d], orow[d]);
+    }
+  }
+  for (int r = 0; r < nr; ++r)
+    for (int d = 0; d < D; ++d) o_rows[(int64_t)r * D + d] /= l[r];
+}
+
 int oracle_attn_f64(const float* q, const float* k, const float* v, double* o, double* lse, int B,
                     int H, int N, int D, double scale, int causal, int mutation) {
   if (B < 1 || H < 1 || N < 1 || D < 1) return -1;
   int err = 0;
+  if (mutation != ORACLE_MUT_NONE) {
+    /* planted mistakes (small test shapes only): one row at a time */
+#pragma omp parallel
+    {
+      double* s = (double*)malloc(sizeof(double) * (size_t)N);
+      if (!s) {
+#pragma omp atomic write
+        err = -3;
+      } else {
+#pragma omp for schedule(dynamic, 4) collapse(2)
+        for (int bh = 0; bh < B * H; ++bh)
+          for (int i = 0; i < N; ++i) {
+            const int64_t off = (int64_t)bh * N * D;
+            row_f64(q + off, k + off, v + off, N, D, scale, causal, mutation, i, s,
+                    o + off + (int64_t)i * D, lse + (int64_t)bh * N + i);
+          }
+        free(s);
+      }
+    }
+    return err;
+  }
+  const int nblk = (N + ORACLE_RB - 1) / ORACLE_RB;
 #pragma omp parallel
   {
-    double* s = (double*)malloc(sizeof(double) * (size_t)N);
-    if (!s) {
+    double* s = (double*)malloc(sizeof(double) * (size_t)N * ORACLE_RB);
+    double* qt = (double*)malloc(sizeof(double) * (size_t)D * ORACLE_RB);
+    if (!s || !qt) {
 #pragma omp atomic write
       err = -3;
     } else {
-#pragma omp for schedule(dynamic, 4) collapse(2)
-      for (int bh = 0; bh < B * H; ++bh)
-        for (int i = 0; i < N; ++i) {
+      /* longest causal blocks (the last ones) first */
+#pragma omp for schedule(dynamic, 1) collapse(2)
+      for (int bi = 0; bi < nblk; ++bi)
+        for (int bh = 0; bh < B * H; ++bh) {
+          const int blk = nblk - 1 - bi;
+          const int i0 = blk * ORACLE_RB;
+          const int nr = N - i0 < ORACLE_RB ? N - i0 : ORACLE_RB;
           const int64_t off = (int64_t)bh * N * D;
-          row_f64(q + off, k + off, v + off, N, D, scale, causal, mutation, i, s,
-                  o + off + (int64_t)i * D, lse + (int64_t)bh * N + i);
+          rows_block_f64(q + off, k + off, v + off, N, D, scale, causal, i0, nr, qt, s,
+                         o + off + (int64_t)i0 * D, lse + (int64_t)bh * N + i0);
         }
-      free(s);
     }
+    free(s);
+    free(qt);
   }
   return err;
 }
@@ -308,7 +421,7 @@ static void row_kernel_numerics(const float* qh, const float* kb, const float* v
     l *= alpha;
     for (int d = 0; d < D; ++d) acc[d] *= alpha;
     for (int j = t0; j < t1; ++j) {
-      const float p = exp2f(s[j - t0] * c - m_use * c); /* :13-15 */
+      const float p = exp2f(fmaf(s[j - t0], c, -(m_use * c))); /* :13-15 */
       l += p;                                           /* unrounded p (:135-152) */
       const float pr = round_to(p, dtype);              /* P -> fp16/bf16 RNE */
       for (int d = 0; d < D; ++d) acc[d] = fmaf(pr, vb[(int64_t)j * D + d], acc[d]);
@@ -320,30 +433,131 @@ static void row_kernel_numerics(const float* qh, const float* kb, const float* v
   if (lse) *lse = (m == -INFINITY ? 0.0f : m) * scale + logf(l);
 }
 
+/* The emulation for rows [i0, i0 + nr) of one head at once (nr <=
+ * ORACLE_RB), for the same reason as rows_block_f64: the rows' score dot
+ * products against one key are independent chains.  Each row keeps
+ * row_kernel_numerics' arithmetic exactly, so every output equals it bit for
+ * bit.  Scratch: qt D x ORACLE_RB floats, s ORACLE_RB x block_n, acc
+ * ORACLE_RB x D. */
+static void rows_block_kernel_numerics(const float* qh, const float* kb, const float* vb, int N,
+                                       int D, float scale, int causal, int dtype, int block_n,
+                                       int i0, int nr, float* qt, float* s, float* acc,
+                                       float* o_rows, float* lse_rows) {
+  const float c = scale * 1.4426950408889634f; /* config.cuh:84 */
+  for (int d = 0; d < D; ++d)
+    for (int r = 0; r < ORACLE_RB; ++r)
+      qt[d * ORACLE_RB + r] = r < nr ? qh[(int64_t)(i0 + r) * D + d] : 0.0f;
+  float m[ORACLE_RB], l[ORACLE_RB];
+  for (int r = 0; r < ORACLE_RB; ++r) {
+    m[r] = -INFINITY;
+    l[r] = 0.0f;
+  }
+  for (int64_t x = 0; x < (int64_t)ORACLE_RB * D; ++x) acc[x] = 0.0f;
+  for (int t0 = 0; t0 < N; t0 += block_n) {
+    const int t1 = t0 + block_n < N ? t0 + block_n : N;
+    if (causal && t0 > i0 + nr - 1) break; /* masked for every row of the block */
+    int j = t0;
+    /* four keys x 16 rows: 8 independent 8-wide fma chains */
+    for (; j + 3 < t1; j += 4) {
+      const float* kr = kb + (int64_t)j * D;
+      __m256 a[4][2];
+      for (int u = 0; u < 4; ++u) a[u][0] = a[u][1] = _mm256_setzero_ps();
+      for (int d = 0; d < D; ++d) {
+        const float* qd = qt + d * ORACLE_RB;
+        const __m256 q0 = _mm256_loadu_ps(qd), q1 = _mm256_loadu_ps(qd + 8);
+        for (int u = 0; u < 4; ++u) {
+          const __m256 x = _mm256_set1_ps(kr[(int64_t)u * D + d]);
+          a[u][0] = _mm256_fmadd_ps(q0, x, a[u][0]);
+          a[u][1] = _mm256_fmadd_ps(q1, x, a[u][1]);
+        }
+      }
+      for (int u = 0; u < 4; ++u) {
+        float au[ORACLE_RB];
+        _mm256_storeu_ps(au, a[u][0]);
+        _mm256_storeu_ps(au + 8, a[u][1]);
+        for (int r = 0; r < ORACLE_RB; ++r) s[(int64_t)r * block_n + (j + u - t0)] = au[r];
+      }
+    }
+    for (; j < t1; ++j) {
+      const float* kr = kb + (int64_t)j * D;
+      float a[ORACLE_RB];
+      for (int r = 0; r < ORACLE_RB; ++r) a[r] = 0.0f;
+      for (int d = 0; d < D; ++d) {
+        const float x = kr[d];
+        const float* qd = qt + d * ORACLE_RB;
+        for (int r = 0; r < ORACLE_RB; ++r) a[r] = fmaf(qd[r], x, a[r]);
+      }
+      for (int r = 0; r < ORACLE_RB; ++r) s[(int64_t)r * block_n + (j - t0)] = a[r];
+    }
+    for (int r = 0; r < nr; ++r) {
+      const int i = i0 + r;
+      if (causal && t0 > i) continue; /* fully masked tile for this row: skipped */
+      float* sr = s + (int64_t)r * block_n;
+      float mt = m[r];
+      for (int j = t0; j < t1; ++j) {
+        if (causal && j > i) sr[j - t0] = -INFINITY;
+        mt = fmaxf(mt, sr[j - t0]);
+      }
+      const float m_use = mt == -INFINITY ? 0.0f : mt;
+      const float alpha = exp2f((m[r] - m_use) * c); /* online_softmax.cuh:17-19 */
+      l[r] *= alpha;
+      float* ar = acc + (int64_t)r * D;
+      for (int d = 0; d < D; ++d) ar[d] *= alpha;
+      for (int j = t0; j < t1; ++j) {
+        const float p = exp2f(fmaf(sr[j - t0], c, -(m_use * c))); /* :13-15 */
+        l[r] += p;                                               /* unrounded p (:135-152) */
+        sr[j - t0] = round_to(p, dtype); /* P -> fp16/bf16 RNE, in place */
+      }
+      m[r] = mt;
+    }
+    for (int j = t0; j < t1; ++j) {
+      const float* vr = vb + (int64_t)j * D;
+      for (int r = 0; r < nr; ++r) {
+        if (causal && t0 > i0 + r) continue;
+        const float pr = s[(int64_t)r * block_n + (j - t0)];
+        float* ar = acc + (int64_t)r * D;
+        for (int d = 0; d < D; ++d) ar[d] = fmaf(pr, vr[d], ar[d]);
+      }
+    }
+  }
+  for (int r = 0; r < nr; ++r) {
+    const float inv_l = 1.0f / l[r];
+    for (int d = 0; d < D; ++d)
+      o_rows[(int64_t)r * D + d] = round_to(acc[(int64_t)r * D + d] * inv_l, dtype);
+    if (lse_rows) lse_rows[r] = (m[r] == -INFINITY ? 0.0f : m[r]) * scale + logf(l[r]);
+  }
+}
+
 int oracle_kernel_numerics(const float* q, const float* k, const float* v, float* o, float* lse,
                            int B, int H, int N, int D, float scale, int causal, int dtype,
                            int block_n) {
   if (B < 1 || H < 1 || N < 1 || D < 1 || block_n < 1) return -1;
   int err = 0;
+  const int nblk = (N + ORACLE_RB - 1) / ORACLE_RB;
 #pragma omp parallel
   {
-    float* acc = (float*)malloc(sizeof(float) * (size_t)D);
-    float* s = (float*)malloc(sizeof(float) * (size_t)block_n);
-    if (!acc || !s) {
+    float* qt = (float*)malloc(sizeof(float) * (size_t)D * ORACLE_RB);
+    float* s = (float*)malloc(sizeof(float) * (size_t)block_n * ORACLE_RB);
+    float* acc = (float*)malloc(sizeof(float) * (size_t)D * ORACLE_RB);
+    if (!qt || !s || !acc) {
 #pragma omp atomic write
       err = -3;
     } else {
-#pragma omp for schedule(dynamic, 4) collapse(2)
-      for (int bh = 0; bh < B * H; ++bh)
-        for (int i = 0; i < N; ++i) {
+#pragma omp for schedule(dynamic, 1) collapse(2)
+      for (int bi = 0; bi < nblk; ++bi)
+        for (int bh = 0; bh < B * H; ++bh) {
+          const int blk = nblk - 1 - bi; /* longest causal blocks first */
+          const int i0 = blk * ORACLE_RB;
+          const int nr = N - i0 < ORACLE_RB ? N - i0 : ORACLE_RB;
           const int64_t off = (int64_t)bh * N * D;
-          row_kernel_numerics(q + off, k + off, v + off, N, D, scale, causal, dtype, block_n, i,
-                              acc, s, o + off + (int64_t)i * D,
-                              lse ? lse + (int64_t)bh * N + i : NULL);
+          rows_block_kernel_numerics(q + off, k + off, v + off, N, D, scale, causal, dtype,
+                                     block_n, i0, nr, qt, s, acc, o + off + (int64_t)i0 * D,
+                                     lse ? lse + (int64_t)bh * N + i0 : NULL);
         }
     }
-    free(acc);
+    free(qt);
     free(s);
+    free(acc);
   }
   return err;
 }

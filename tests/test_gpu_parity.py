@@ -39,11 +39,14 @@ def _fwd(fa, q, k, v, causal, scale=None):
 def _check_against_oracle(oracle, q, k, v, o, lse, causal, scale, dtype, contract=True):
     """contract=True: the north-star bars (max-abs 1e-2, mean-abs 1e-3, 2x the
     emulated reference-kernel error, LSE 1e-3), stated for and holding on the
-    BASELINE configurations, where |O| is small.  contract=False (explicit
-    scales, random problems): peaked rows put |O| above 1, where bf16's
-    rounding of P and of O alone (the reference kernel's arithmetic, which
-    the emulator reproduces) exceeds 1e-2; those cases are held to the 2x
-    reference-kernel bar on the mean error (3x on the max) and to the LSE bar."""
+    BASELINE configurations, where |O| is small.
+
+    contract=False (explicit scales, score jumps, random problems): peaked
+    rows put |O| above 1, where one rounding of a bf16 output alone (the
+    reference kernel's own arithmetic, which the emulator reproduces) can
+    exceed 1e-2.  Those cases keep every relative bar (max-abs and mean-abs
+    <= 2x the emulated reference kernel's, LSE <= 1e-3); the absolute max-abs
+    bar 1e-2 holds for fp16 and scales with max(1, max|O|) for bf16."""
     qn, kn, vn = to_np32(q), to_np32(k), to_np32(v)
     ref_o, ref_lse = oracle.attn_f64(qn, kn, vn, scale, causal)
     emu_o, _ = oracle.kernel_numerics(qn, kn, vn, scale, causal,
@@ -60,13 +63,10 @@ def _check_against_oracle(oracle, q, k, v, o, lse, causal, scale, dtype, contrac
         assert mean <= MEAN_ABS_TOL, f"mean-abs {mean}"
     elif dtype == "fp16":
         assert mx <= MAX_ABS_TOL, f"max-abs {mx}"
-    # The maximum over ~1e4 elements is one rounding event of P or O: which
-    # elements round badly depends on the exponent offset, and this kernel's
-    # lazy offset differs from the reference's per-tile one.  Outside the
-    # contract configurations the max is held to 3x, the mean to 2x.
-    max_factor = 2 if contract else 3
-    assert mx <= max_factor * emx + 1e-6, \
-        f"max-abs {mx} > {max_factor}x reference-kernel error {emx}"
+    else:
+        o_scale = max(1.0, float(np.abs(ref_o).max()))
+        assert mx <= MAX_ABS_TOL * o_scale, f"max-abs {mx} (max|O| {o_scale})"
+    assert mx <= 2 * emx + 1e-6, f"max-abs {mx} > 2x reference-kernel error {emx}"
     assert mean <= 2 * emean + 1e-6, f"mean-abs {mean} > 2x reference-kernel error {emean}"
     assert lse_err <= LSE_TOL, f"lse {lse_err}"
 
@@ -272,60 +272,39 @@ def _sample_rows(N, H_total, rng, n_random=48):
     return heads, sel_bh, sel_row
 
 
+@pytest.mark.timeout(900)
 @pytest.mark.parametrize("name", ["C2", "C3", "C4", "C5", "C5r"])
-def test_config_sampled_rows_vs_oracle(fa, oracle, name):
-    """Full-size BASELINE configs: selected rows of selected heads against the
-    fp64 oracle, and the whole output against the convex-hull bound."""
+def test_config_full_vs_oracle(fa, oracle, name):
+    """Full-size BASELINE configs, every element: the whole O and LSE against
+    the fp64 oracle (max-abs <= 1e-2, mean-abs <= 1e-3, LSE <= 1e-3), the
+    whole O against 2x the emulated reference kernel's max-abs and mean-abs
+    error on the same inputs, as the reference's own gates compare every
+    element (benchmark/cpp/correctness_v6.cu:74-104,
+    benchmark/python/tests/test_pybind_correctness.py:114-131)."""
     B, H, N, D, dtype, causal, sigma, case = CONFIGS[name]
-    _note(f"case {name} {B}x{H}x{N}x{D} {dtype} causal={causal}")
+    _note(f"case {name} {B}x{H}x{N}x{D} {dtype} causal={causal} (full tensor)")
     q, k, v, causal, scale = make_config(name, device=DEV)
     o, lse = _fwd(fa, q, k, v, causal)
-    assert torch.isfinite(o).all().item()
-    assert torch.isfinite(lse).all().item()
-
-    rng = np.random.default_rng(case)
-    heads, sel_bh, sel_row = _sample_rows(N, B * H, rng)
-    # Oracle inputs: only the selected heads (flattened b*H + h).
-    qf = q.reshape(B * H, N, D)
-    kf = k.reshape(B * H, N, D)
-    vf = v.reshape(B * H, N, D)
-    hsel = torch.tensor(heads, device=DEV)
-    qn = to_np32(qf[hsel])[None]
-    kn = to_np32(kf[hsel])[None]
-    vn = to_np32(vf[hsel])[None]
-    remap = {h: i for i, h in enumerate(heads)}
-    local_bh = np.array([remap[h] for h in sel_bh], np.int32)
-    ref_o, ref_lse = oracle.attn_rows_f64(qn, kn, vn, scale, causal, local_bh, sel_row)
-    got_o = to_np32(o.reshape(B * H, N, D)[torch.tensor(sel_bh, device=DEV).long(),
-                                           torch.tensor(sel_row, device=DEV).long()])
-    got_lse = to_np32(lse.reshape(B * H, N)[torch.tensor(sel_bh, device=DEV).long(),
-                                            torch.tensor(sel_row, device=DEV).long()])
-    emu_o, _ = oracle.kernel_numerics_rows(qn, kn, vn, scale, causal, local_bh, sel_row,
-                                           oracle.BF16 if dtype == "bf16" else oracle.F16)
+    got_o = to_np32(o)
+    got_lse = to_np32(lse)
+    qn, kn, vn = to_np32(q), to_np32(k), to_np32(v)
+    del o, lse, q, k, v
+    torch.cuda.empty_cache()
+    assert np.isfinite(got_o).all() and np.isfinite(got_lse).all()
+    ref_o, ref_lse = oracle.attn_f64(qn, kn, vn, scale, causal)
     mx, mean = err_stats(got_o, ref_o)
-    emx, emean = err_stats(emu_o, ref_o)
     lse_err = float(np.abs(got_lse.astype(np.float64) - ref_lse).max())
-    _note(f"  sampled {len(sel_row)} rows: max_abs={mx:.3e} mean_abs={mean:.3e} "
-          f"(ref-kernel emu {emx:.3e}/{emean:.3e}) lse={lse_err:.3e}")
-    assert mx <= MAX_ABS_TOL
-    assert mean <= MEAN_ABS_TOL
+    _note(f"  oracle: max_abs={mx:.3e} mean_abs={mean:.3e} lse={lse_err:.3e} "
+          f"over {got_o.size} elements")
+    assert mx <= MAX_ABS_TOL, f"max-abs {mx}"
+    assert mean <= MEAN_ABS_TOL, f"mean-abs {mean}"
+    assert lse_err <= LSE_TOL, f"lse {lse_err}"
+    emu_o, _ = oracle.kernel_numerics(qn, kn, vn, scale, causal,
+                                      oracle.BF16 if dtype == "bf16" else oracle.F16)
+    emx, emean = err_stats(emu_o, ref_o)
+    _note(f"  reference-kernel emulator: max_abs={emx:.3e} mean_abs={emean:.3e}")
     assert mx <= 2 * emx + 1e-6, f"max-abs {mx} > 2x reference-kernel error {emx}"
     assert mean <= 2 * emean + 1e-6, f"mean-abs {mean} > 2x reference-kernel error {emean}"
-    assert lse_err <= LSE_TOL
-
-    # Every O row is a convex combination of the visible V rows: per head dim,
-    # it lies within [min, max] of V over those rows (prefix for causal).
-    vf32 = v.float()
-    if causal:
-        vmax = torch.cummax(vf32, dim=2).values
-        vmin = torch.cummin(vf32, dim=2).values
-    else:
-        vmax = vf32.amax(dim=2, keepdim=True)
-        vmin = vf32.amin(dim=2, keepdim=True)
-    of = o.float()
-    margin = 4e-3 * torch.maximum(vmax.abs(), vmin.abs()) + 1e-3
-    assert bool((of <= vmax + margin).all().item()), "O above the convex hull of V"
-    assert bool((of >= vmin - margin).all().item()), "O below the convex hull of V"
 
 
 @pytest.mark.parametrize("pattern", ["ramp", "drop"])
@@ -354,7 +333,7 @@ def test_score_jumps_long_causal_sampled_rows(fa, oracle, pattern):
           f"(ref-kernel emu {emx:.3e}/{emean:.3e}) lse={lse_err:.3e}")
     assert np.isfinite(got_o).all()
     assert mx <= MAX_ABS_TOL
-    assert mx <= 3 * emx + 1e-6 and mean <= 2 * emean + 1e-6
+    assert mx <= 2 * emx + 1e-6 and mean <= 2 * emean + 1e-6
     assert lse_err <= LSE_TOL
 
 

@@ -96,5 +96,5 @@ def test_random_plans_vs_oracle(fa, oracle, lib, case):
     lse_err = float(np.abs(got_lse.astype(np.float64) - ref_lse).max())
     _note(f"  {len(sel_row)} rows: max_abs={mx:.3e} mean_abs={mean:.3e} "
           f"(ref-kernel emu {emx:.3e}/{emean:.3e}) lse={lse_err:.3e}")
-    assert mx <= 3 * emx + 1e-6 and mean <= 2 * emean + 1e-6
+    assert mx <= 2 * emx + 1e-6 and mean <= 2 * emean + 1e-6
     assert lse_err <= LSE_TOL

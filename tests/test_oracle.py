@@ -166,3 +166,80 @@ def test_round_bf16_matches_torch(oracle):
     ref = torch.from_numpy(x).to(torch.bfloat16)
     assert np.array_equal(bits, ref.view(torch.int16).numpy().view(np.uint16))
     assert np.array_equal(got, ref.float().numpy())
+
+
+# ---------------------------------------------------------------------------
+# Pin of the reference-kernel emulator's rounding.  With V rows one-hot
+# (V[j] = e_j) and integer Q, K (exact fp32 scores), the emulator's output
+# exposes every rounded P: O[i][j] = round_out(P_j * alpha-rescaled / l).  The
+# restatement below follows the reference's arithmetic in numpy
+# (online_softmax.cuh:13-19 p = exp2(s*c - m*c), :17-19 alpha, :89-152 the
+# rescale and the sum l of the unrounded p; forward_v6_mma.cuh:19-38 P
+# rounded RNE to the input type before P V; :206-234 O normalised in fp32 and
+# rounded), tile by tile.  The emulator must equal it on every element, and a
+# restatement that rounds P to the other 16-bit type must not.
+
+
+def _round_t(x, dt):
+    t = torch.from_numpy(np.ascontiguousarray(x, np.float32))
+    return t.to(dt).float().numpy()
+
+
+def _restated_one_hot(qi, ki, scale, p_dtype, o_dtype, block_n=64, l_rounded=False):
+    """Emulator arithmetic for V = one-hot rows, restated per tile in numpy
+    (l_rounded: a planted mistake, l summed over the rounded P)."""
+    N, D = ki.shape
+    s = (qi.astype(np.int64) @ ki.astype(np.int64).T).astype(np.float64)  # exact
+    c = np.float32(np.float32(scale) * np.float32(1.4426950408889634))
+    out = np.zeros((qi.shape[0], D), np.float32)
+    for i in range(qi.shape[0]):
+        m = np.float32(-np.inf)
+        l = np.float32(0.0)
+        acc = np.zeros(D, np.float32)
+        for t0 in range(0, N, block_n):
+            st = s[i, t0:t0 + block_n]
+            mt = np.float32(max(float(m), float(st.max())))
+            with np.errstate(invalid="ignore"):
+                a_arg = np.float32((m - mt) * c)
+            alpha = np.float32(np.exp2(np.float64(a_arg)))
+            l = np.float32(l * alpha)
+            acc = (acc * alpha).astype(np.float32)
+            mc = np.float64(np.float32(mt * c))
+            x = (st * np.float64(c) - mc).astype(np.float32)  # fmaf(s, c, -(m*c))
+            p = np.exp2(x.astype(np.float64)).astype(np.float32)
+            pr = _round_t(p, p_dtype)
+            for pj in (pr if l_rounded else p):
+                l = np.float32(l + pj)
+            acc[t0:t0 + len(st)] = (acc[t0:t0 + len(st)] + pr).astype(np.float32)
+            m = mt
+        inv = np.float32(np.float32(1.0) / l)
+        out[i] = _round_t(acc * inv, o_dtype)
+    return out
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+@pytest.mark.parametrize("N,D", [(48, 64), (128, 128)])
+def test_kernel_numerics_rounding_pinned(oracle, dtype, N, D):
+    rng = np.random.default_rng(N + D)
+    qi = rng.integers(-3, 4, size=(N, D))
+    ki = rng.integers(-3, 4, size=(N, D))
+    v = np.zeros((N, D), np.float32)
+    v[np.arange(N), np.arange(N)] = 1.0
+    scale = 0.05
+    tdt, other = ((torch.float16, torch.bfloat16) if dtype == "fp16"
+                  else (torch.bfloat16, torch.float16))
+    q4 = qi.astype(np.float32)[None, None]
+    k4 = ki.astype(np.float32)[None, None]
+    eo, _ = oracle.kernel_numerics(q4, k4, v[None, None], scale, False,
+                                   oracle.BF16 if dtype == "bf16" else oracle.F16)
+    eo = eo[0, 0]
+    # every output value is representable in the output type (O is rounded)
+    assert np.array_equal(_round_t(eo, tdt), eo)
+    ref = _restated_one_hot(qi, ki, scale, tdt, tdt)
+    assert np.array_equal(eo, ref)
+    # P rounded to the other 16-bit type: visibly different
+    wrong = _restated_one_hot(qi, ki, scale, other, tdt)
+    assert (wrong[:, :N] != eo[:, :N]).mean() > 0.1
+    # l summed over the rounded P instead of the unrounded p: also visible
+    wrong_l = _restated_one_hot(qi, ki, scale, tdt, tdt, l_rounded=True)
+    assert (wrong_l[:, :N] != eo[:, :N]).mean() > 0.01

@@ -70,7 +70,7 @@ def check_table(pl, B, H, N, D, causal, cus=256):
     k = len(split_q)
     assert split_q == set(range(nq - k, nq))
     assert pl.n_merge == k and pl.n_slots == 2 * k
-    assert pl.workspace_bytes == B * H * 2 * k * BM * (D * 4 + 8)
+    assert pl.workspace_bytes == B * H * 2 * k * BM * (D * 4 + 16)
     assert n == hpx * (nq + k)
     lens = [pl.tile_end[i] - pl.tile_begin[i] for i in range(n)]
     m = max(n - cpx, 0)
@@ -120,7 +120,7 @@ def check_plan(pl, B, H, N, D, causal):
     # dispatch order: longest first
     lens = [te - tb for _, tb, te, _, _ in items]
     assert lens == sorted(lens, reverse=True)
-    assert pl.workspace_bytes == B * H * pl.n_slots * BM * (D * 4 + 8)
+    assert pl.workspace_bytes == B * H * pl.n_slots * BM * (D * 4 + 16)
     # the split shortens the longest work item
     assert max(lens) < max(tiles(qb, N, BM, causal) for qb in range(nq))
 
@@ -240,5 +240,5 @@ def test_workspace_bound(lib):
     the plan never asks for more than B*H*128*256*(128*4+8) bytes."""
     for N in (2048, 3000, 4096, 8192, 16384):
         pl = plan(lib, contiguous(B=1, H=1, N=N, D=128, causal=0))
-        assert pl.workspace_bytes <= 128 * 256 * (128 * 4 + 8)
+        assert pl.workspace_bytes <= 128 * 256 * (128 * 4 + 16)
         assert pl.n_slots <= A.FA_PLAN_MAX_ITEMS
