@@ -337,6 +337,24 @@ fa_status fa_fwd_ws_timed(const fa_fwd_params* p, void* workspace, uint64_t work
   return launch_timed(p, workspace, workspace_bytes, stream, ms);
 }
 
+fa_status fa_fwd_scratch(const fa_fwd_params* p, void* stream) {
+  static_assert(fa::kScratchBytes == FA_SCRATCH_BYTES, "header and library disagree");
+  uint64_t need = 0;
+  const fa_status s = fa_fwd_workspace_size(p, &need);
+  if (s != FA_OK) return s;
+  if (need == 0) return launch(p, nullptr, 0, stream);
+  if (need > fa::kScratchBytes)
+    return fail(FA_ERR_UNSUPPORTED,
+                "the split-KV plan needs %llu bytes of workspace; the static scratch holds %llu "
+                "(use fa_fwd_ws with a caller workspace, or fa_fwd)",
+                (unsigned long long)need, (unsigned long long)fa::kScratchBytes);
+  void* ws = nullptr;
+  const hipError_t e = fa::scratch_buffer(&ws);
+  if (e != hipSuccess)
+    return fail(FA_ERR_HIP, "scratch lookup failed: %s", hipGetErrorString(e));
+  return launch(p, ws, fa::kScratchBytes, stream);
+}
+
 fa_status fa_device_info(int device, fa_device_info_t* out) {
   if (out == nullptr) return fail(FA_ERR_NULL, "out is NULL");
   std::memset(out, 0, sizeof(*out));

@@ -82,4 +82,11 @@ size_t plan_split(const KernelArgs& args, int compute_units, bool allow_split, S
 // kernel and the merge kernel.
 hipError_t launch_fwd(const KernelArgs& args, hipStream_t stream);
 
+// Bytes of the library's static split-KV scratch array (per device).
+constexpr size_t kScratchBytes = size_t(32) << 20;
+
+// Device address of that array on the calling thread's current device
+// (hipGetSymbolAddress on the first call per device, then cached).
+hipError_t scratch_buffer(void** ptr);
+
 }  // namespace fa

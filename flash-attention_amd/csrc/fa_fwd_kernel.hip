@@ -67,8 +67,17 @@
 #include <cmath>
 #include <type_traits>
 
+#include <atomic>
+#include <mutex>
+
 #include "fa_device_ops.h"
 #include "fa_fwd_kernel.h"
+
+// Split-KV workspace of fa_fwd_scratch, for callers that cannot allocate:
+// one array per GPU the library runs on, held until the process ends.  Host
+// code never passes `scratch` itself (its host-side name is not a device
+// address); it uses the address scratch_buffer() obtains per device.
+static __device__ __align__(256) char scratch[fa::kScratchBytes];
 
 namespace fa {
 namespace {
@@ -962,6 +971,32 @@ size_t plan_split(const KernelArgs& a, int compute_units, bool allow_split, Spli
     plan->n_items = plan->n_slots = plan->n_merge = 0;
   }
   return plan_xcd_table(a, compute_units, allow_split, plan);
+}
+
+hipError_t scratch_buffer(void** ptr) {
+  // Device address of `scratch` on each device, looked up once per device
+  // (with that device current) and kept.
+  constexpr int kMaxDevices = 64;
+  static std::atomic<void*> addr[kMaxDevices];
+  static std::mutex lock;
+  *ptr = nullptr;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  void* p = addr[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    std::lock_guard<std::mutex> g(lock);
+    p = addr[dev].load(std::memory_order_acquire);
+    if (p == nullptr) {
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess) return e;
+      if (p == nullptr) return hipErrorInvalidSymbol;
+      addr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *ptr = p;
+  return hipSuccess;
 }
 
 hipError_t launch_fwd(const KernelArgs& a, hipStream_t stream) {

@@ -23,6 +23,8 @@
  *                        fa_fwd / fa_fwd_timed add split-KV for problems
  *                        whose grid would leave most CUs idle behind a few
  *                        long q-tiles (short causal sequences, few heads).
+ *   - fa_fwd_scratch:    no counterpart in the reference; fa_fwd_ws for
+ *                        callers that cannot allocate (see its comment).
  *
  * Semantics (all entry points):
  *   O[b,h,i,:] = sum_j softmax_j(scale * Q[b,h,i,:].K[b,h,j,:] + mask_ij) V[b,h,j,:]
@@ -35,9 +37,12 @@
  * and optional.
  *
  * Ownership: all pointers are borrowed; the library allocates no device memory
- * (the split-KV partials live in a workspace the caller provides).
+ * (the split-KV partials live in a workspace the caller provides, or, for
+ * fa_fwd_scratch, in a static array of FA_SCRATCH_BYTES per device).
  * Threading: re-entrant; the only mutable global state is a thread-local error
- * string and a per-device cache of the CU count (written once, atomically).
+ * string, a per-device cache of the CU count (written once, atomically), the
+ * per-device address of the scratch array (looked up once, under a lock) and
+ * that array's contents (fa_fwd_scratch only).
  * Streams: fa_fwd is asynchronous on `stream`; unlike the reference
  * kernel, an unsupported argument never turns into a silent device no-op —
  * it is rejected on the host with a status code before anything is launched.
@@ -159,6 +164,23 @@ fa_status fa_fwd_ws(const fa_fwd_params* p, void* workspace, uint64_t workspace_
 /* fa_fwd_ws bracketed by two HIP events on `stream`, as fa_fwd_timed. */
 fa_status fa_fwd_ws_timed(const fa_fwd_params* p, void* workspace, uint64_t workspace_bytes,
                           void* stream, float* ms);
+
+/* Bytes of the library's static split-KV scratch (one array per device). */
+#define FA_SCRATCH_BYTES (32ull << 20)
+
+/* fa_fwd_ws with the library's own static device scratch array as the
+ * workspace: allocates nothing (no hipMalloc, no allocating library call).
+ * No counterpart in the reference; it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid allocation).  The array (FA_SCRATCH_BYTES per device) is
+ * reserved on every device the library runs on until the process ends; its
+ * address is looked up on the first call per device.  A problem whose
+ * split-KV plan needs more than FA_SCRATCH_BYTES is rejected with
+ * FA_ERR_UNSUPPORTED and nothing is launched.  Every call on one device
+ * shares that device's array, which keeps the last call's contents: calls
+ * that overlap on one device (other streams, other host threads) race and
+ * must be ordered by the caller.  Same results as fa_fwd_ws. */
+fa_status fa_fwd_scratch(const fa_fwd_params* p, void* stream);
 
 /* The work plan fa_fwd_ws would use for *p on a device with
  * `compute_units` CUs (split-KV, or an XCD placement table, or none).

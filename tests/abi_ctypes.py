@@ -19,6 +19,7 @@ LIB_PATH = os.path.join(REPO_ROOT, "flash-attention_amd", "flash_attention_runti
 FA_OK, FA_ERR_NULL, FA_ERR_DTYPE, FA_ERR_SHAPE, FA_ERR_HEADDIM, FA_ERR_STRIDE, \
     FA_ERR_UNSUPPORTED, FA_ERR_HIP, FA_ERR_ARG = range(9)
 FA_DTYPE_F16, FA_DTYPE_BF16 = 0, 1
+FA_SCRATCH_BYTES = 32 << 20  # include/fa_mi355x.h
 
 
 class FaFwdParams(ctypes.Structure):
@@ -99,6 +100,8 @@ def load(path: str = LIB_PATH):
     L.fa_fwd_ws_timed.argtypes = [P, ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p,
                                   ctypes.POINTER(ctypes.c_float)]
     L.fa_fwd_ws_timed.restype = ctypes.c_int
+    L.fa_fwd_scratch.argtypes = [P, ctypes.c_void_p]
+    L.fa_fwd_scratch.restype = ctypes.c_int
     L.fa_fwd_plan.argtypes = [P, ctypes.c_int32, ctypes.POINTER(FaFwdPlan)]
     L.fa_fwd_plan.restype = ctypes.c_int
     L.fa_status_str.argtypes = [ctypes.c_int]
