@@ -72,6 +72,7 @@
 
 #include "fa_device_ops.h"
 #include "fa_fwd_kernel.h"
+#include "fa_lds_layout.h"
 
 // Split-KV workspace of fa_fwd_scratch, for callers that cannot allocate:
 // one array per GPU the library runs on, held until the process ends.  Host
@@ -85,37 +86,8 @@ namespace {
 using namespace dev;
 
 
-template <int D>
-struct Tile {
-  static constexpr int BN = 64;                 // keys per K/V tile
-  static constexpr int ROWB = D * 2;            // bytes per K/V row
-  static constexpr int BYTES = BN * ROWB;       // bytes per K or V tile
-  // K tile: the 32x32x16 A-operand read is ds_read_b128 of one 16-byte chunk
-  // per lane for 32 consecutive keys; XOR the chunk index with key bits so
-  // consecutive keys land on distinct bank groups.
-  static __device__ __forceinline__ int swz_k(int key) {
-    return D == 128 ? (key & 15) : ((key >> 1) & 7);
-  }
-  // V tile: a transposed read covers 4 consecutive keys x 64 contiguous bytes
-  // per half-wave; XOR the 64-byte segment so the 4 keys hit distinct banks.
-  static __device__ __forceinline__ int swz_v(int key) {
-    return D == 128 ? ((key & 3) << 2) : (((key >> 1) & 1) << 2);
-  }
-};
-
-// Where lane `lane` of wave `wave` lands in a K/V LDS tile for DMA
-// instruction `it`: tile row r and the logical 16-byte chunk it must fetch
-// (the XOR swizzle is applied on the source side because a DMA lane's LDS
-// destination is fixed at base + 16*lane).
-template <int D, int NW, bool IS_V>
-__device__ __forceinline__ void dma_slot(int wave, int it, int lane, int& r, int& c) {
-  using T = Tile<D>;
-  constexpr int ITERS = T::BYTES / (1024 * NW);
-  const int off = (wave * ITERS + it) * 1024 + lane * 16;
-  r = off / T::ROWB;
-  const int pc = (off % T::ROWB) / 16;
-  c = pc ^ (IS_V ? T::swz_v(r) : T::swz_k(r));
-}
+using lds::Tile;
+using lds::dma_slot;
 
 // Lazy exponent offset.  The offset m in p = exp2(s*c - m*c) is re-derived
 // from the row max only when a tile's P sum (per lane, 32 keys) reaches
@@ -334,24 +306,15 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
   const f16x8 sum_sel = row_sum_selector(lane);
 
   // Per-lane LDS byte offsets inside a tile (loop invariant).
-  // K: A operand of key block kb, k-step kk -> row kb*32 + l32, chunk 2kk+g.
+  // K: A operand of key block 0, k-step kk (block 1: + 32 rows).
   int k_off[KSTEPS];
 #pragma unroll
-  for (int kk = 0; kk < KSTEPS; ++kk)
-    k_off[kk] = l32 * T::ROWB + (((2 * kk + g) ^ T::swz_k(l32)) << 4);
-  // V^T: transposed read for 16-key chunk ch, half hf, head-dim block db:
-  // this lane supplies row key = 16ch + 8hf + 4g + (lj>>2) and
-  // columns 32db + 16hg + 4(lj&3) .. +3.
+  for (int kk = 0; kk < KSTEPS; ++kk) k_off[kk] = lds::k_read_offset<D>(0, kk, lane);
+  // V^T: transposed read of chunk 0, half 0, head-dim block db (other chunks
+  // and halves: + 16ch + 8hf rows, as immediates).
   uint32_t v_addr[DBLK];
-  {
-    const int key = 4 * g + (lj >> 2);  // + 16ch + 8hf: multiples of 4 keep swz_v
 #pragma unroll
-    for (int db = 0; db < DBLK; ++db) {
-      const int col = 32 * db + 16 * hg + 4 * (lj & 3);
-      const int chunk = col >> 3;
-      v_addr[db] = smem_base + key * T::ROWB + ((chunk ^ T::swz_v(key)) << 4) + (col & 7) * 2;
-    }
-  }
+  for (int db = 0; db < DBLK; ++db) v_addr[db] = smem_base + lds::v_read_offset<D>(0, 0, db, lane);
 
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();

@@ -1,0 +1,96 @@
+// LDS layout of the K and V tiles of the forward kernel: where the staging
+// DMA puts each lane's 16 bytes, the XOR swizzles, and the byte offsets the
+// MFMA operand reads use.  Shared by the kernel (fa_fwd_kernel.hip, device
+// code) and the CPU layout checks (tests/lds/, host code), so the checks run
+// the same functions the kernel runs.
+//
+// Replaces the reference's smem layout (src/loadstore/copy_gsm.cuh:31-47
+// smem_offset_g2s, src/loadstore/copy_srm.cuh:14-30 smem_offset,
+// src/tensor_core/swizzle.cuh:5-28 Swizzle<3,3,3>), which is built for 32-bank
+// NVIDIA shared memory and ldmatrix; this one is derived for the gfx950 LDS
+// and the reads below.
+#pragma once
+
+#if defined(__HIPCC__)
+#include <hip/hip_runtime.h>
+#define FA_LAYOUT_FN __host__ __device__ __forceinline__
+#else
+#define FA_LAYOUT_FN inline
+#endif
+
+// Bits cleared from the K / V swizzles.  Always 0 in the library; the CPU
+// layout checks build a copy with one bit cleared to show they detect it.
+#ifndef FA_LDS_SWZ_K_CLEAR
+#define FA_LDS_SWZ_K_CLEAR 0
+#endif
+#ifndef FA_LDS_SWZ_V_CLEAR
+#define FA_LDS_SWZ_V_CLEAR 0
+#endif
+
+namespace fa {
+namespace lds {
+
+template <int D>
+struct Tile {
+  static constexpr int BN = 64;            // keys per K/V tile
+  static constexpr int ROWB = D * 2;       // bytes per K/V row
+  static constexpr int BYTES = BN * ROWB;  // bytes per K or V tile
+  // K tile: the 32x32x16 A-operand read is ds_read_b128 of one 16-byte chunk
+  // per lane for 32 consecutive keys; XOR the chunk index with key bits so
+  // consecutive keys land on distinct bank groups.
+  static FA_LAYOUT_FN int swz_k(int key) {
+    return (D == 128 ? (key & 15) : ((key >> 1) & 7)) & ~FA_LDS_SWZ_K_CLEAR;
+  }
+  // V tile: a transposed read covers 4 consecutive keys x 64 contiguous bytes
+  // per half-wave; XOR the 64-byte segment so the 4 keys hit distinct banks.
+  static FA_LAYOUT_FN int swz_v(int key) {
+    return (D == 128 ? ((key & 3) << 2) : (((key >> 1) & 1) << 2)) & ~FA_LDS_SWZ_V_CLEAR;
+  }
+};
+
+// Where lane `lane` of wave `wave` lands in a K/V LDS tile for DMA
+// instruction `it`: tile row r and the logical 16-byte chunk it must fetch.
+// The LDS destination of a DMA lane is fixed at base + 16*lane (the
+// instruction's base is byte (wave*ITERS + it)*1024 of the tile), so the XOR
+// swizzle is applied to the source chunk instead.
+template <int D, int NW, bool IS_V>
+FA_LAYOUT_FN void dma_slot(int wave, int it, int lane, int& r, int& c) {
+  using T = Tile<D>;
+  constexpr int ITERS = T::BYTES / (1024 * NW);
+  const int off = (wave * ITERS + it) * 1024 + lane * 16;
+  r = off / T::ROWB;
+  const int pc = (off % T::ROWB) / 16;
+  c = pc ^ (IS_V ? T::swz_v(r) : T::swz_k(r));
+}
+
+// Byte offset within a K tile of the 16 bytes lane `lane` reads (one
+// ds_read_b128) as the A operand of S^T = K Q^T for key block kb (32 keys)
+// and k-step kk: key kb*32 + lane%32, head dims [16kk + 8(lane/32), +8).
+// Keys of block 1 sit 32 rows below block 0 with the same swizzle bits, so
+// the kernel adds kb*32*ROWB to the block-0 offset.
+template <int D>
+FA_LAYOUT_FN int k_read_offset(int kb, int kk, int lane) {
+  using T = Tile<D>;
+  const int key = kb * 32 + (lane & 31);
+  const int chunk = 2 * kk + (lane >> 5);
+  return key * T::ROWB + ((chunk ^ T::swz_k(key)) << 4);
+}
+
+// Byte offset within a V tile of the 8 bytes lane `lane` addresses with one
+// ds_read_b64_tr_b16 for the V^T operand of 16-key chunk ch, half hf and
+// 32-wide head-dim block db.  The lane supplies row key = 16ch + 8hf +
+// 4(lane/32) + (lane%16)/4 and columns 32db + 16((lane/16)%2) + 4(lane%4) ..
+// +3 (the transposing read hands lane i of each 16-lane group element i%4
+// of the words addressed by lanes 4e + i/4).  Multiples of 4 keys keep the
+// swizzle bits, so the kernel adds ch*16*ROWB + hf*8*ROWB as immediates.
+template <int D>
+FA_LAYOUT_FN int v_read_offset(int ch, int hf, int db, int lane) {
+  using T = Tile<D>;
+  const int lj = lane & 15, hg = (lane >> 4) & 1, g = lane >> 5;
+  const int key = 16 * ch + 8 * hf + 4 * g + (lj >> 2);
+  const int col = 32 * db + 16 * hg + 4 * (lj & 3);
+  return key * T::ROWB + (((col >> 3) ^ T::swz_v(key)) << 4) + (col & 7) * 2;
+}
+
+}  // namespace lds
+}  // namespace fa

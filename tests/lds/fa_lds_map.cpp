@@ -1,0 +1,61 @@
+// Host build of the kernel's LDS layout functions (flash-attention_amd/csrc/
+// fa_lds_layout.h) for the CPU layout checks in tests/test_lds_layout.py.
+// Test infrastructure: never linked into the library.
+#include "fa_lds_layout.h"
+
+namespace {
+
+template <int D, int NW, bool IS_V>
+int dma_map(int* r, int* c) {
+  constexpr int ITERS = fa::lds::Tile<D>::BYTES / (1024 * NW);
+  int n = 0;
+  for (int w = 0; w < NW; ++w)
+    for (int it = 0; it < ITERS; ++it)
+      for (int lane = 0; lane < 64; ++lane, ++n) fa::lds::dma_slot<D, NW, IS_V>(w, it, lane, r[n], c[n]);
+  return n;
+}
+
+template <int D>
+int k_reads(int* off) {
+  int n = 0;
+  for (int kb = 0; kb < 2; ++kb)
+    for (int kk = 0; kk < D / 16; ++kk)
+      for (int lane = 0; lane < 64; ++lane) off[n++] = fa::lds::k_read_offset<D>(kb, kk, lane);
+  return n;
+}
+
+template <int D>
+int v_reads(int* off) {
+  int n = 0;
+  for (int ch = 0; ch < 4; ++ch)
+    for (int hf = 0; hf < 2; ++hf)
+      for (int db = 0; db < D / 32; ++db)
+        for (int lane = 0; lane < 64; ++lane) off[n++] = fa::lds::v_read_offset<D>(ch, hf, db, lane);
+  return n;
+}
+
+}  // namespace
+
+extern "C" {
+
+// (row, logical chunk) fetched by DMA lane (wave, it, lane), in that order;
+// returns the number of entries (NW * ITERS * 64) or -1 for an unknown shape.
+int fa_lds_dma_map(int D, int NW, int is_v, int* r, int* c) {
+  if (D == 128 && NW == 4) return is_v ? dma_map<128, 4, true>(r, c) : dma_map<128, 4, false>(r, c);
+  if (D == 128 && NW == 8) return is_v ? dma_map<128, 8, true>(r, c) : dma_map<128, 8, false>(r, c);
+  if (D == 64 && NW == 4) return is_v ? dma_map<64, 4, true>(r, c) : dma_map<64, 4, false>(r, c);
+  if (D == 64 && NW == 8) return is_v ? dma_map<64, 8, true>(r, c) : dma_map<64, 8, false>(r, c);
+  return -1;
+}
+
+// K operand read offsets [kb 2][kk D/16][lane 64].
+int fa_lds_k_reads(int D, int* off) {
+  return D == 128 ? k_reads<128>(off) : D == 64 ? k_reads<64>(off) : -1;
+}
+
+// V^T operand read offsets [ch 4][hf 2][db D/32][lane 64].
+int fa_lds_v_reads(int D, int* off) {
+  return D == 128 ? v_reads<128>(off) : D == 64 ? v_reads<64>(off) : -1;
+}
+
+}  // extern "C"

@@ -1,0 +1,189 @@
+"""CPU checks of the K/V tile layout in LDS (flash-attention_amd/csrc/
+fa_lds_layout.h), on a host build of the same functions the kernel runs
+(tests/lds/fa_lds_map.cpp, compiled here with g++).
+
+For D in {64, 128} and workgroups of 4 and 8 waves:
+- the staging DMA covers every (key, 16-byte chunk) of a tile exactly once
+  (a bijection onto the tile's bytes);
+- every K operand read (ds_read_b128, A operand of S^T = K Q^T) and every V^T
+  operand read (ds_read_b64_tr_b16) finds the bytes the DMA put there for
+  the key and head dims the MFMA lane maps require;
+- the offsets the kernel uses for key block 1 and for later V chunks/halves
+  (a constant added to block 0 / chunk 0) equal the general formula;
+- no read has a bank conflict, under this model of the gfx950 LDS: 64 banks
+  of 4 bytes, a wave's read served 256 bytes at a time in lane order (16
+  lanes of a ds_read_b128, 32 lanes of a ds_read_b64_tr_b16), and two lanes
+  of one group conflict when they touch the same bank at different
+  addresses.  The model agrees with the measured SQ_LDS_BANK_CONFLICT = 0 of
+  the current layout (profiles/fa_fwd_C3_counters.md);
+- the bank check sees a dropped swizzle bit: a copy built with one bit of the
+  K or V swizzle cleared still reads what it wrote, but conflicts.
+
+Reference counterpart: the swizzle offset known-answer tests of
+tests/unit/layout/test_tile_to_shape_runtime.cu:152-168 (for the NVIDIA
+Swizzle<3,3,3> layout, which this build does not use).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+REPO = os.path.dirname(HERE)
+CSRC = os.path.join(REPO, "flash-attention_amd", "csrc")
+SRC = os.path.join(HERE, "lds", "fa_lds_map.cpp")
+
+BANKS, BANK_BYTES = 64, 4
+
+
+def _build(out_dir, defines=()):
+    out = os.path.join(out_dir, "libfa_lds_map_%d.so" % abs(hash(defines)))
+    cmd = ["g++", "-O1", "-std=c++17", "-shared", "-fPIC", "-I", CSRC,
+           *[f"-D{d}" for d in defines], SRC, "-o", out]
+    subprocess.run(cmd, check=True)
+    lib = ctypes.CDLL(out)
+    ip = ctypes.POINTER(ctypes.c_int)
+    lib.fa_lds_dma_map.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ip, ip]
+    lib.fa_lds_k_reads.argtypes = [ctypes.c_int, ip]
+    lib.fa_lds_v_reads.argtypes = [ctypes.c_int, ip]
+    return lib
+
+
+@pytest.fixture(scope="module")
+def lib(tmp_path_factory):
+    return _build(str(tmp_path_factory.mktemp("lds")))
+
+
+def _ptr(a):
+    return a.ctypes.data_as(ctypes.POINTER(ctypes.c_int))
+
+
+def _dma_slots(lib, D, NW, is_v):
+    """slot[key, chunk] = LDS byte offset (within the tile) the DMA writes it
+    to.  A DMA lane's destination is fixed by the instruction: byte
+    (wave*ITERS + it)*1024 + 16*lane of the tile, in the map's order."""
+    rowb = 2 * D
+    n = 64 * rowb // 16
+    r = np.empty(n, np.int32)
+    c = np.empty(n, np.int32)
+    assert lib.fa_lds_dma_map(D, NW, int(is_v), _ptr(r), _ptr(c)) == n
+    slot = np.full((64, rowb // 16), -1, np.int64)
+    dest = np.arange(n, dtype=np.int64) * 16
+    assert ((r >= 0) & (r < 64) & (c >= 0) & (c < rowb // 16)).all()
+    slot[r, c] = dest
+    return slot, r, c
+
+
+def _k_reads(lib, D):
+    ks = D // 16
+    off = np.empty(2 * ks * 64, np.int32)
+    assert lib.fa_lds_k_reads(D, _ptr(off)) == off.size
+    return off.reshape(2, ks, 64).astype(np.int64)
+
+
+def _v_reads(lib, D):
+    nd = D // 32
+    off = np.empty(4 * 2 * nd * 64, np.int32)
+    assert lib.fa_lds_v_reads(D, _ptr(off)) == off.size
+    return off.reshape(4, 2, nd, 64).astype(np.int64)
+
+
+def _conflicts(addrs, nbytes, group):
+    """Bank conflicts of one wave-wide read: lanes served `group` at a time,
+    each lane touching `nbytes` bytes from its address.  Counts, per group,
+    the bank accesses beyond one distinct address per bank."""
+    total = 0
+    for g0 in range(0, len(addrs), group):
+        seen = {}
+        for a in addrs[g0:g0 + group]:
+            for w in range(0, nbytes, BANK_BYTES):
+                word = (int(a) + w) // BANK_BYTES
+                seen.setdefault(word % BANKS, set()).add(word)
+        total += sum(len(s) - 1 for s in seen.values())
+    return total
+
+
+CASES = [(D, NW) for D in (64, 128) for NW in (4, 8)]
+
+
+@pytest.mark.parametrize("D,NW", CASES)
+@pytest.mark.parametrize("is_v", [False, True], ids=["K", "V"])
+def test_dma_is_a_bijection_onto_the_tile(lib, D, NW, is_v):
+    slot, r, c = _dma_slots(lib, D, NW, is_v)
+    assert (slot >= 0).all(), "some (key, chunk) is never staged"
+    pairs = r.astype(np.int64) * (2 * D // 16) + c
+    assert np.unique(pairs).size == pairs.size, "some (key, chunk) is staged twice"
+
+
+@pytest.mark.parametrize("D,NW", CASES)
+def test_k_reads_find_the_staged_keys(lib, D, NW):
+    slot, _, _ = _dma_slots(lib, D, NW, False)
+    off = _k_reads(lib, D)
+    lane = np.arange(64)
+    for kb in range(2):
+        for kk in range(D // 16):
+            # 32x32x16 A operand: lane l supplies row l % 32 (the key) and
+            # k-elements 8(l / 32) .. +7 of k-step kk (head dims 16kk + ...).
+            key = kb * 32 + lane % 32
+            chunk = 2 * kk + lane // 32
+            assert np.array_equal(off[kb, kk], slot[key, chunk]), (kb, kk)
+    # the kernel's form: block 1 = block 0 + 32 rows
+    assert np.array_equal(off[1], off[0] + 32 * 2 * D)
+
+
+@pytest.mark.parametrize("D,NW", CASES)
+def test_v_reads_find_the_staged_keys(lib, D, NW):
+    slot, _, _ = _dma_slots(lib, D, NW, True)
+    off = _v_reads(lib, D)
+    lane = np.arange(64)
+    lj, hg, g = lane % 16, (lane // 16) % 2, lane // 32
+    for ch in range(4):
+        for hf in range(2):
+            for db in range(D // 32):
+                key = 16 * ch + 8 * hf + 4 * g + lj // 4
+                col = 32 * db + 16 * hg + 4 * (lj % 4)
+                want = slot[key, col // 8] + (col % 8) * 2
+                assert np.array_equal(off[ch, hf, db], want), (ch, hf, db)
+                # the kernel's form: chunk/half offsets added as immediates
+                assert np.array_equal(off[ch, hf, db], off[0, 0, db] + (16 * ch + 8 * hf) * 2 * D)
+
+
+def _read_conflicts(lib, D):
+    k = _k_reads(lib, D)
+    v = _v_reads(lib, D)
+    kc = sum(_conflicts(k[kb, kk], 16, 16) for kb in range(2) for kk in range(D // 16))
+    vc = sum(_conflicts(v[ch, hf, db], 8, 32)
+             for ch in range(4) for hf in range(2) for db in range(D // 32))
+    return kc, vc
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_reads_are_bank_conflict_free(lib, D):
+    assert _read_conflicts(lib, D) == (0, 0)
+
+
+def test_dma_writes_are_bank_conflict_free():
+    # each DMA instruction writes 64 lanes x 16 contiguous bytes
+    assert _conflicts(np.arange(64) * 16, 16, 16) == 0
+
+
+@pytest.mark.parametrize("D,k_clear,v_clear", [(128, 8, 0), (128, 1, 0), (128, 0, 4),
+                                               (128, 0, 8), (64, 4, 0), (64, 1, 0),
+                                               (64, 0, 4)])
+def test_dropped_swizzle_bit_is_detected(tmp_path, D, k_clear, v_clear):
+    """One swizzle bit cleared: reads still find what the DMA wrote (both
+    sides share the swizzle), but the bank check reports conflicts."""
+    mut = _build(str(tmp_path), (f"FA_LDS_SWZ_K_CLEAR={k_clear}", f"FA_LDS_SWZ_V_CLEAR={v_clear}"))
+    slot, _, _ = _dma_slots(mut, D, 4, False)
+    off = _k_reads(mut, D)
+    lane = np.arange(64)
+    assert np.array_equal(off[0, 0], slot[lane % 32, lane // 32])
+    kc, vc = _read_conflicts(mut, D)
+    if k_clear:
+        assert kc > 0, "a dropped K swizzle bit went unnoticed"
+    if v_clear:
+        assert vc > 0, "a dropped V swizzle bit went unnoticed"
