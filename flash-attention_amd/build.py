@@ -4,6 +4,7 @@ Outputs (next to the Python package, so they travel with the repository):
   flash_attention_runtime/libfa_mi355x.so   HIP kernels + C ABI (hipcc, gfx950)
   flash_attention_runtime/_C<EXT_SUFFIX>     torch/pybind binding over the C ABI
   flash_attention_runtime/fa_profile         C++ benchmark CLI over the C ABI
+  flash_attention_runtime/fa_device_query    device description CLI over the C ABI
   flash_attention_runtime/fa_mfma_probe      MFMA-only throughput probe (peak cross-check)
 
 Replaces the reference's JIT build (python/flash_attention_runtime/
@@ -62,12 +63,14 @@ def _hipcc() -> str:
 
 
 def build_hip_library(jobs: int) -> str:
-    """Compiles every csrc/*.hip and fa_api.cpp with hipcc and links the
+    """Compiles csrc/fa_fwd_kernel.hip (kernels and launch), fa_plan.cpp
+    (host work planning) and fa_api.cpp (the C ABI) with hipcc and links the
     shared library libfa_mi355x.so."""
     os.makedirs(BUILD_DIR, exist_ok=True)
     hipcc = _hipcc()
     sources = [
         os.path.join(CSRC, "fa_fwd_kernel.hip"),
+        os.path.join(CSRC, "fa_plan.cpp"),
         os.path.join(CSRC, "fa_api.cpp"),
     ]
     objs = []
@@ -125,6 +128,17 @@ def build_profile_cli() -> str:
     return out
 
 
+def build_device_query() -> str:
+    """Links the fa_device_query executable (csrc/fa_device_query.cpp)
+    against libfa_mi355x.so (rpath $ORIGIN)."""
+    out = os.path.join(OUT_DIR, "fa_device_query")
+    _run([_hipcc(), "-O2", "-std=c++17", "-Wall", "-I", INCLUDE,
+          os.path.join(CSRC, "fa_device_query.cpp"), f"-L{OUT_DIR}", "-lfa_mi355x",
+          "-Wl,-rpath,$ORIGIN", "-o", out + ".tmp"])
+    os.replace(out + ".tmp", out)
+    return out
+
+
 def build_mfma_probe() -> str:
     """Builds the fa_mfma_probe executable (csrc/fa_mfma_probe.hip), which
     times MFMA-only waves to cross-check the computed MFMA peak."""
@@ -139,8 +153,9 @@ def build(jobs: int = 8) -> list[str]:
     lib = build_hip_library(jobs)
     ext = build_torch_binding()
     cli = build_profile_cli()
+    query = build_device_query()
     probe = build_mfma_probe()
-    return [lib, ext, cli, probe]
+    return [lib, ext, cli, query, probe]
 
 
 def main() -> None:

@@ -371,6 +371,15 @@ fa_status fa_device_info(int device, fa_device_info_t* out) {
   out->l2_bytes = prop.l2CacheSize;
   out->memory_bus_width_bits = prop.memoryBusWidth;
   out->memory_clock_khz = prop.memoryClockRate;
+  out->global_mem_bytes = (int64_t)prop.totalGlobalMem;
+  out->lds_per_block_bytes = (int64_t)prop.sharedMemPerBlock;
+  out->regs_per_block = prop.regsPerBlock;
+  out->regs_per_cu = prop.regsPerMultiprocessor;
+  out->max_threads_per_cu = prop.maxThreadsPerMultiProcessor;
+  out->max_threads_per_block = prop.maxThreadsPerBlock;
+  out->wavefront_size = prop.warpSize;
+  out->arch_major = prop.major;
+  out->arch_minor = prop.minor;
   // CDNA4: 2048 dense fp16/bf16 FMA = 4096 flop per clock per CU.
   out->fp16_dense_peak_tflops = (double)prop.multiProcessorCount * prop.clockRate * 1e3 * 4096.0 / 1e12;
   // The DDR formula below does not hold for HBM3E's data rate; for gfx950

@@ -68,10 +68,16 @@ struct KernelArgs {
   SplitPlan split;
 };
 
+// Non-causal problems with at least this many keys use 8-wave workgroups;
+// causal fp16 problems from kWideCausalMinSeq keys on.
+constexpr int kWideMinSeq = 2048;
+constexpr int kWideCausalMinSeq = 8192;
+
 // Workgroup rows (BM) of the kernel variant launch_fwd picks for args.
 int block_rows(const KernelArgs& args);
 
-// Computes the work plan for args on a device with `compute_units` CUs.
+// Computes the work plan for args on a device with `compute_units` CUs
+// (host code, fa_plan.cpp).
 // With allow_split it may choose split-KV and returns the workspace bytes it
 // needs; otherwise (or when no split pays) it returns 0 and leaves either no
 // plan (n_items = 0) or an XCD placement table (xcd_heads > 0).

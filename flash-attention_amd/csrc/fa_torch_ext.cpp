@@ -140,6 +140,15 @@ pybind11::dict device_info(int device) {
   d["memory_clock_khz"] = info.memory_clock_khz;
   d["fp16_dense_peak_tflops"] = info.fp16_dense_peak_tflops;
   d["hbm_peak_gbps"] = info.hbm_peak_gbps;
+  d["global_mem_bytes"] = info.global_mem_bytes;
+  d["lds_per_block_bytes"] = info.lds_per_block_bytes;
+  d["regs_per_block"] = info.regs_per_block;
+  d["regs_per_cu"] = info.regs_per_cu;
+  d["max_threads_per_cu"] = info.max_threads_per_cu;
+  d["max_threads_per_block"] = info.max_threads_per_block;
+  d["wavefront_size"] = info.wavefront_size;
+  d["arch_major"] = info.arch_major;
+  d["arch_minor"] = info.arch_minor;
   return d;
 }
 

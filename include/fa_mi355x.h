@@ -107,6 +107,17 @@ typedef struct {
   /* published 8000 GB/s for gfx950 (MI355X); 2 x bus width x memory clock
    * (DDR) for other devices */
   double hbm_peak_gbps;
+  /* the remaining fields of utils/get_gpu_hardware_param.cu:11-24 */
+  int64_t global_mem_bytes;      /* totalGlobalMem */
+  int64_t lds_per_block_bytes;   /* sharedMemPerBlock */
+  int32_t regs_per_block;        /* regsPerBlock */
+  int32_t regs_per_cu;           /* regsPerMultiprocessor */
+  int32_t max_threads_per_cu;    /* maxThreadsPerMultiProcessor */
+  int32_t max_threads_per_block; /* maxThreadsPerBlock */
+  int32_t wavefront_size;        /* warpSize (64 on CDNA) */
+  int32_t arch_major;            /* major (gfx9xx: 9) */
+  int32_t arch_minor;            /* minor */
+  int32_t reserved;
 } fa_device_info_t;
 
 /* Split-KV plan of a problem (diagnostic; filled by fa_fwd_plan). */

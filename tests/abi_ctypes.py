@@ -13,8 +13,10 @@ import re
 
 REPO_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(REPO_ROOT, "include", "fa_mi355x.h")
-LIB_PATH = os.path.join(REPO_ROOT, "flash-attention_amd", "flash_attention_runtime",
-                        "libfa_mi355x.so")
+# FA_MI355X_LIB: another build of the library to test (tests/test_abi_asan.py
+# points it at an AddressSanitizer build of the host code).
+LIB_PATH = os.environ.get("FA_MI355X_LIB") or os.path.join(
+    REPO_ROOT, "flash-attention_amd", "flash_attention_runtime", "libfa_mi355x.so")
 
 FA_OK, FA_ERR_NULL, FA_ERR_DTYPE, FA_ERR_SHAPE, FA_ERR_HEADDIM, FA_ERR_STRIDE, \
     FA_ERR_UNSUPPORTED, FA_ERR_HIP, FA_ERR_ARG = range(9)
@@ -55,6 +57,16 @@ class FaDeviceInfo(ctypes.Structure):
         ("memory_clock_khz", ctypes.c_int32),
         ("fp16_dense_peak_tflops", ctypes.c_double),
         ("hbm_peak_gbps", ctypes.c_double),
+        ("global_mem_bytes", ctypes.c_int64),
+        ("lds_per_block_bytes", ctypes.c_int64),
+        ("regs_per_block", ctypes.c_int32),
+        ("regs_per_cu", ctypes.c_int32),
+        ("max_threads_per_cu", ctypes.c_int32),
+        ("max_threads_per_block", ctypes.c_int32),
+        ("wavefront_size", ctypes.c_int32),
+        ("arch_major", ctypes.c_int32),
+        ("arch_minor", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
     ]
 
 

@@ -107,7 +107,11 @@ int main(void) {
   F(fa_device_info_t, clock_khz); F(fa_device_info_t, lds_per_cu_bytes);
   F(fa_device_info_t, l2_bytes); F(fa_device_info_t, memory_bus_width_bits);
   F(fa_device_info_t, memory_clock_khz); F(fa_device_info_t, fp16_dense_peak_tflops);
-  F(fa_device_info_t, hbm_peak_gbps);
+  F(fa_device_info_t, hbm_peak_gbps); F(fa_device_info_t, global_mem_bytes);
+  F(fa_device_info_t, lds_per_block_bytes); F(fa_device_info_t, regs_per_block);
+  F(fa_device_info_t, regs_per_cu); F(fa_device_info_t, max_threads_per_cu);
+  F(fa_device_info_t, max_threads_per_block); F(fa_device_info_t, wavefront_size);
+  F(fa_device_info_t, arch_major); F(fa_device_info_t, arch_minor); F(fa_device_info_t, reserved);
   F(fa_fwd_plan_t, block_rows); F(fa_fwd_plan_t, n_items); F(fa_fwd_plan_t, n_slots);
   F(fa_fwd_plan_t, n_merge); F(fa_fwd_plan_t, xcd_heads); F(fa_fwd_plan_t, workspace_bytes);
   F(fa_fwd_plan_t, q_tile); F(fa_fwd_plan_t, tile_begin); F(fa_fwd_plan_t, tile_end);
