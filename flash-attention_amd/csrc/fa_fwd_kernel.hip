@@ -37,6 +37,9 @@
 //    q-tiles of the same heads.  Causal grids of one round follow an XCD
 //    placement table instead (longest q-tiles alone on a CU, the others
 //    paired long with short; see plan_xcd_table).
+//  * O (and the fp32 split partials) leave through LDS: each wave parks its
+//    32-row tile in the then idle K/V ring and stores whole rows, 16
+//    contiguous bytes per lane.
 //  * Split-KV (with a caller workspace, when a few long q-tiles would set
 //    the time of a short grid): a q-tile's key tiles are cut into chunks
 //    computed by separate workgroups, which write fp32 partials (O, m, l);
@@ -550,47 +553,91 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
   }
 
   const bool row_ok = qrow < N;
+  // The output goes out through LDS, whole rows at a time.  In the O^T
+  // accumulator a lane holds 4 consecutive head dims of one row per (db, r),
+  // so a direct store instruction writes 32 rows in 8- or 16-byte pieces;
+  // staged, each store instruction writes 64 / (row bytes / 16) whole rows
+  // with 16 contiguous bytes per lane (+9 % at B4 H16 N1024 D64, +1..2 % at
+  // B4 H32 N4096).  The K/V ring is free: the loop ended with a barrier and
+  // staged nothing after it.  Each wave uses rows [32 wave, +32) of the ring
+  // as a 32-row tile with `rowb`-byte rows whose 16-byte chunks are XOR
+  // swizzled by the row (row r's chunk c at c ^ (r % chunks)); a wave reads
+  // back only what it wrote, so no barrier is needed.
+  auto store_rows = [&](int rowb, auto&& put, char* dst, int64_t dst_stride, int rows)
+                        FA_INLINE {
+    const int nc = rowb >> 4;
+    char* ot = smem + wave * 32 * rowb;
+    put([&](int r, int c, int half, auto w) FA_INLINE {
+      *reinterpret_cast<decltype(w)*>(ot + r * rowb + ((c ^ (r & (nc - 1))) << 4) +
+                                      half * sizeof(w)) = w;
+    });
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the tile is in LDS
+    const int rpi = 64 / nc;             // rows per read
+    const int rr = lane / nc, cc = lane & (nc - 1);
+#pragma unroll
+    for (int j = 0; j < 32 / rpi; ++j) {
+      const int r = j * rpi + rr;
+      const u32x4 w = *reinterpret_cast<const u32x4*>(ot + r * rowb + ((cc ^ (r & (nc - 1))) << 4));
+      if (r < rows) *reinterpret_cast<u32x4*>(dst + r * dst_stride + cc * 16) = w;
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // the reads are done before the ring is reused
+  };
+  const int wave_rows = max(0, min(32, N - wrow0));  // rows of this wave below N
+
   if (SPLIT && n_chunks > 1) {
     // ---- split-KV partial: unnormalised O, offset m (raw score units; -inf
     // when no key of this chunk is visible to the row), the row sum l for the
     // LSE and the sum of the rounded P for the normalisation ----
     const int64_t slot =
         (int64_t)(args.split.xcd_heads > 0 ? args.split.part[item] : args.split.slot[item]) + chunk;
-    const int64_t row = ((int64_t)bh * args.split.n_slots + slot) * BM + (qrow - q0);
-    if (row_ok) {
-      float* po = args.ws_o + row * D;
+    const int64_t row0 = ((int64_t)bh * args.split.n_slots + slot) * BM + (wrow0 - q0);
+    // fp32 rows of 4D bytes: NW / 4 passes of DBLK / (NW / 4) head-dim
+    // blocks each fit the ring (NW x 32 x 4D / passes <= 4 x 64 x 2D).
+    constexpr int PASSES = NW / 4, PDB = DBLK / PASSES;
+    static_for<0, PASSES>([&](auto p_c) {
+      constexpr int p = decltype(p_c)::value;
+      store_rows(
+          PDB * 128,
+          [&](auto&& put) FA_INLINE {
 #pragma unroll
-      for (int db = 0; db < DBLK; ++db)
+            for (int b = 0; b < PDB; ++b)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int col = 32 * db + 8 * r + 4 * g;
-          const f32x4 w = {o_acc[db][4 * r + 0], o_acc[db][4 * r + 1], o_acc[db][4 * r + 2],
-                           o_acc[db][4 * r + 3]};
-          *reinterpret_cast<f32x4*>(po + col) = w;
-        }
-      if (g == 0)
-        *reinterpret_cast<f32x4*>(args.ws_ml + row * 4) = f32x4{m_run, l_tot, lr_tot, 0.0f};
+              for (int r = 0; r < 4; ++r) {
+                const int db = p * PDB + b;
+                const f32x4 w = {o_acc[db][4 * r + 0], o_acc[db][4 * r + 1], o_acc[db][4 * r + 2],
+                                 o_acc[db][4 * r + 3]};
+                // cols 32b + 8r + 4g of the pass: chunk 8b + 2r + g
+                put(l32, 8 * b + 2 * r + g, 0, w);
+              }
+          },
+          reinterpret_cast<char*>(args.ws_o + row0 * D + p * PDB * 32), int64_t(4 * D), wave_rows);
+    });
+    if (row_ok && g == 0) {
+      const int64_t row = row0 + l32;
+      *reinterpret_cast<f32x4*>(args.ws_ml + row * 4) = f32x4{m_run, l_tot, lr_tot, 0.0f};
     }
     return;
   }
 
   // ---- epilogue: normalise, store ----
   const float inv_l = (row_ok && lr_tot > 0.0f) ? 1.0f / lr_tot : 0.0f;
-  if (row_ok) {
-    char* op = oh + qrow * osb;
+  store_rows(
+      2 * D,
+      [&](auto&& put) FA_INLINE {
 #pragma unroll
-    for (int db = 0; db < DBLK; ++db)
+        for (int db = 0; db < DBLK; ++db)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int col = 32 * db + 8 * r + 4 * g;
-        u32x2 w = {pack2<BF16>(o_acc[db][4 * r + 0] * inv_l, o_acc[db][4 * r + 1] * inv_l),
-                   pack2<BF16>(o_acc[db][4 * r + 2] * inv_l, o_acc[db][4 * r + 3] * inv_l)};
-        *reinterpret_cast<u32x2*>(op + col * 2) = w;
-      }
-    if (args.lse != nullptr && g == 0) {
-      const float m_use = m_run == -INFINITY ? 0.0f : m_run;
-      args.lse[(int64_t)bh * N + qrow] = m_use * args.scale + __logf(l_tot);
-    }
+          for (int r = 0; r < 4; ++r) {
+            const u32x2 w = {pack2<BF16>(o_acc[db][4 * r + 0] * inv_l, o_acc[db][4 * r + 1] * inv_l),
+                             pack2<BF16>(o_acc[db][4 * r + 2] * inv_l, o_acc[db][4 * r + 3] * inv_l)};
+            // cols 32db + 8r + 4g: chunk 4db + r, half g
+            put(l32, 4 * db + r, g, w);
+          }
+      },
+      oh + wrow0 * osb, osb, wave_rows);
+  if (row_ok && args.lse != nullptr && g == 0) {
+    const float m_use = m_run == -INFINITY ? 0.0f : m_run;
+    args.lse[(int64_t)bh * N + qrow] = m_use * args.scale + __logf(l_tot);
   }
 }
 
