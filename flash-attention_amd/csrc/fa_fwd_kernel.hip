@@ -281,9 +281,33 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
   issue_tile(t_begin, 0);
 
   // Q as the B operand of S^T = K Q^T: lane holds query qrow, dims
-  // [16*kk + 8*g, +8) for k-step kk.
+  // [16*kk + 8*g, +8) for k-step kk.  Read straight from global memory
+  // that is 32 rows x 32 bytes per instruction.  4-wave workgroups instead
+  // stage each wave's 32 rows in LDS with whole-row DMA (16 bytes per lane,
+  // QRB / 16 lanes per row) and read the operands from there once they have
+  // landed (+1.5..2.5 % at B4 H16 N1024 D64 and B1 H16 N3000 causal; the
+  // 8-wave kernel, whose prologue is a small part of a long workgroup, loses
+  // 0.5 % to it and keeps the direct loads).  The staging area, ring
+  // buffers 1 and 3, is free until the first tile_step.  Row r's 16-byte
+  // chunk c sits at c ^ swizzle(r), so the operand reads (32 rows, one chunk
+  // each) are conflict free.  Rows past N re-read row N-1.
+  constexpr bool kStageQ = NW == 4;
+  constexpr int QRB = 2 * D, QNC = QRB / 16;  // bytes and 16-byte chunks per Q row
+  auto q_swz = [](int r) FA_INLINE { return QNC == 16 ? (r & 15) : ((r >> 1) & 7); };
+  const uint32_t q_lds = (uint32_t)((wave < 2 ? 1 : 3) * T::BYTES + (wave & 1) * 32 * QRB);
+  if constexpr (kStageQ) {
+    const int qr0 = min(wrow0, N - 1);
+    const char* qbase = qh + qr0 * qsb;
+#pragma unroll
+    for (int it = 0; it < KSTEPS; ++it) {  // 32 rows x QRB bytes = KSTEPS x 1 KiB
+      const int pos = it * 1024 + lane * 16;
+      const int r = pos / QRB, cs = (pos % QRB) / 16;
+      const int row = min(wrow0 + r, N - 1) - qr0;
+      dma_16b((uint32_t)(row * qsb + (cs ^ q_swz(r)) * 16), qbase, smem_base + q_lds + it * 1024);
+    }
+  }
   i16x8 qf[KSTEPS];
-  {
+  if constexpr (!kStageQ) {
     const int qr = qrow < N ? qrow : N - 1;
     const char* qp = qh + qr * qsb + g * 16;
 #pragma unroll
@@ -315,6 +339,16 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
 #pragma unroll
   for (int db = 0; db < DBLK; ++db) v_addr[db] = smem_base + lds::v_read_offset<D>(0, 0, db, lane);
 
+  if constexpr (kStageQ) {
+    // This wave's Q rows have landed (its own DMA): read the operands, and
+    // finish the reads before the barrier after which tile 1 refills
+    // buffers 1 and 3.
+    __builtin_amdgcn_s_waitcnt(0);
+#pragma unroll
+    for (int kk = 0; kk < KSTEPS; ++kk)
+      qf[kk] = *reinterpret_cast<const i16x8*>(smem + q_lds + l32 * QRB +
+                                               (((2 * kk + g) ^ q_swz(l32)) * 16));
+  }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
