@@ -288,22 +288,24 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
   // landed (+1.5..2.5 % at B4 H16 N1024 D64 and B1 H16 N3000 causal; the
   // 8-wave kernel, whose prologue is a small part of a long workgroup, loses
   // 0.5 % to it and keeps the direct loads).  The staging area, ring
-  // buffers 1 and 3, is free until the first tile_step.  Row r's 16-byte
-  // chunk c sits at c ^ swizzle(r), so the operand reads (32 rows, one chunk
+  // buffers 1 and 3, is free until the first tile_step.  The rows form an
+  // lds::row_tile_offset tile, so the operand reads (32 rows, one chunk
   // each) are conflict free.  Rows past N re-read row N-1.
   constexpr bool kStageQ = NW == 4;
-  constexpr int QRB = 2 * D, QNC = QRB / 16;  // bytes and 16-byte chunks per Q row
-  auto q_swz = [](int r) FA_INLINE { return QNC == 16 ? (r & 15) : ((r >> 1) & 7); };
+  constexpr int QRB = 2 * D;  // bytes per Q row
   const uint32_t q_lds = (uint32_t)((wave < 2 ? 1 : 3) * T::BYTES + (wave & 1) * 32 * QRB);
   if constexpr (kStageQ) {
     const int qr0 = min(wrow0, N - 1);
     const char* qbase = qh + qr0 * qsb;
 #pragma unroll
     for (int it = 0; it < KSTEPS; ++it) {  // 32 rows x QRB bytes = KSTEPS x 1 KiB
+      // DMA lane destinations are fixed (16 bytes per lane): fetch the chunk
+      // that belongs at this position.
       const int pos = it * 1024 + lane * 16;
       const int r = pos / QRB, cs = (pos % QRB) / 16;
       const int row = min(wrow0 + r, N - 1) - qr0;
-      dma_16b((uint32_t)(row * qsb + (cs ^ q_swz(r)) * 16), qbase, smem_base + q_lds + it * 1024);
+      dma_16b((uint32_t)(row * qsb + (cs ^ lds::row_swz(r, QRB)) * 16), qbase,
+              smem_base + q_lds + it * 1024);
     }
   }
   i16x8 qf[KSTEPS];
@@ -346,8 +348,8 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
     __builtin_amdgcn_s_waitcnt(0);
 #pragma unroll
     for (int kk = 0; kk < KSTEPS; ++kk)
-      qf[kk] = *reinterpret_cast<const i16x8*>(smem + q_lds + l32 * QRB +
-                                               (((2 * kk + g) ^ q_swz(l32)) * 16));
+      qf[kk] = *reinterpret_cast<const i16x8*>(smem + q_lds +
+                                               lds::row_tile_offset(l32, 2 * kk + g, QRB));
   }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
@@ -594,16 +596,16 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
   // with 16 contiguous bytes per lane (+9 % at B4 H16 N1024 D64, +1..2 % at
   // B4 H32 N4096).  The K/V ring is free: the loop ended with a barrier and
   // staged nothing after it.  Each wave uses rows [32 wave, +32) of the ring
-  // as a 32-row tile with `rowb`-byte rows whose 16-byte chunks are XOR
-  // swizzled by the row (row r's chunk c at c ^ (r % chunks)); a wave reads
-  // back only what it wrote, so no barrier is needed.
+  // as an lds::row_tile_offset tile of 32 `rowb`-byte rows, written and
+  // read 16 bytes per lane (the LDS serves 8-byte accesses one dword at a
+  // time across the wave, so 8-byte pieces would hit even banks only); a
+  // wave reads back only what it wrote, so no barrier is needed.
   auto store_rows = [&](int rowb, auto&& put, char* dst, int64_t dst_stride, int rows)
                         FA_INLINE {
     const int nc = rowb >> 4;
     char* ot = smem + wave * 32 * rowb;
-    put([&](int r, int c, int half, auto w) FA_INLINE {
-      *reinterpret_cast<decltype(w)*>(ot + r * rowb + ((c ^ (r & (nc - 1))) << 4) +
-                                      half * sizeof(w)) = w;
+    put([&](int r, int c, auto w) FA_INLINE {
+      *reinterpret_cast<decltype(w)*>(ot + lds::row_tile_offset(r, c, rowb)) = w;
     });
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the tile is in LDS
     const int rpi = 64 / nc;             // rows per read
@@ -611,7 +613,7 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
 #pragma unroll
     for (int j = 0; j < 32 / rpi; ++j) {
       const int r = j * rpi + rr;
-      const u32x4 w = *reinterpret_cast<const u32x4*>(ot + r * rowb + ((cc ^ (r & (nc - 1))) << 4));
+      const u32x4 w = *reinterpret_cast<const u32x4*>(ot + lds::row_tile_offset(r, cc, rowb));
       if (r < rows) *reinterpret_cast<u32x4*>(dst + r * dst_stride + cc * 16) = w;
     }
     __builtin_amdgcn_s_waitcnt(0xc07f);  // the reads are done before the ring is reused
@@ -641,7 +643,7 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
                 const f32x4 w = {o_acc[db][4 * r + 0], o_acc[db][4 * r + 1], o_acc[db][4 * r + 2],
                                  o_acc[db][4 * r + 3]};
                 // cols 32b + 8r + 4g of the pass: chunk 8b + 2r + g
-                put(l32, 8 * b + 2 * r + g, 0, w);
+                put(l32, 8 * b + 2 * r + g, w);
               }
           },
           reinterpret_cast<char*>(args.ws_o + row0 * D + p * PDB * 32), int64_t(4 * D), wave_rows);
@@ -661,11 +663,21 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
 #pragma unroll
         for (int db = 0; db < DBLK; ++db)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const u32x2 w = {pack2<BF16>(o_acc[db][4 * r + 0] * inv_l, o_acc[db][4 * r + 1] * inv_l),
-                             pack2<BF16>(o_acc[db][4 * r + 2] * inv_l, o_acc[db][4 * r + 3] * inv_l)};
-            // cols 32db + 8r + 4g: chunk 4db + r, half g
-            put(l32, 4 * db + r, g, w);
+          for (int k = 0; k < 2; ++k) {
+            // This lane holds 4 columns (half a 16-byte chunk) of row l32 for
+            // each of r = 2k and 2k + 1: cols 32db + 8r + 4g .. +3.  One swap
+            // of lanes l + 32 <-> l (v_permlane32_swap: the upper half of the
+            // first operand with the lower half of the second) leaves lane
+            // (l32, g) with the whole chunk 4db + 2k + g of its row.
+            const f32x16& o = o_acc[db];
+            const int i = 8 * k;
+            const u32x2 a = {pack2<BF16>(o[i + 0] * inv_l, o[i + 1] * inv_l),
+                             pack2<BF16>(o[i + 2] * inv_l, o[i + 3] * inv_l)};
+            const u32x2 b = {pack2<BF16>(o[i + 4] * inv_l, o[i + 5] * inv_l),
+                             pack2<BF16>(o[i + 6] * inv_l, o[i + 7] * inv_l)};
+            const auto x = __builtin_amdgcn_permlane32_swap(a[0], b[0], false, false);
+            const auto y = __builtin_amdgcn_permlane32_swap(a[1], b[1], false, false);
+            put(l32, 4 * db + 2 * k + g, u32x4{x[0], y[0], x[1], y[1]});
           }
       },
       oh + wrow0 * osb, osb, wave_rows);

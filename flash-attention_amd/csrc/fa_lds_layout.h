@@ -26,6 +26,10 @@
 #ifndef FA_LDS_SWZ_V_CLEAR
 #define FA_LDS_SWZ_V_CLEAR 0
 #endif
+// The same for the row tiles: bits cleared from row_swz.
+#ifndef FA_LDS_ROW_SWZ_CLEAR
+#define FA_LDS_ROW_SWZ_CLEAR 0
+#endif
 
 namespace fa {
 namespace lds {
@@ -90,6 +94,19 @@ FA_LAYOUT_FN int v_read_offset(int ch, int hf, int db, int lane) {
   const int key = 16 * ch + 8 * hf + 4 * g + (lj >> 2);
   const int col = 32 * db + 16 * hg + 4 * (lj & 3);
   return key * T::ROWB + (((col >> 3) ^ T::swz_v(key)) << 4) + (col & 7) * 2;
+}
+
+// Row tiles: 32 rows of `rowb` bytes (rowb = 128, 256 or 512) that a wave
+// stages on its own, Q for its MFMA operands (4-wave workgroups) and O or
+// the fp32 split partials on their way out.  Row r's 16-byte chunk c sits at
+// chunk position c ^ row_swz(r).  16-byte writes of one chunk per lane over
+// 32 rows and 16-byte reads of whole rows are then free of bank conflicts.
+FA_LAYOUT_FN int row_swz(int r, int rowb) {
+  const int nc = rowb >> 4;  // chunks per row
+  return (nc >= 16 ? (r & (nc - 1)) : ((r >> 1) & (nc - 1))) & ~FA_LDS_ROW_SWZ_CLEAR;
+}
+FA_LAYOUT_FN int row_tile_offset(int r, int c, int rowb) {
+  return r * rowb + ((c ^ row_swz(r, rowb)) << 4);
 }
 
 }  // namespace lds

@@ -58,4 +58,7 @@ int fa_lds_v_reads(int D, int* off) {
   return D == 128 ? v_reads<128>(off) : D == 64 ? v_reads<64>(off) : -1;
 }
 
+// Row tiles: byte offset of (row r, chunk c) in a 32-row tile of rowb-byte rows.
+int fa_lds_row_offset(int r, int c, int rowb) { return fa::lds::row_tile_offset(r, c, rowb); }
+
 }  // extern "C"

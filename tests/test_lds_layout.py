@@ -17,7 +17,11 @@ For D in {64, 128} and workgroups of 4 and 8 waves:
   addresses.  The model agrees with the measured SQ_LDS_BANK_CONFLICT = 0 of
   the current layout (profiles/fa_fwd_C3_counters.md);
 - the bank check sees a dropped swizzle bit: a copy built with one bit of the
-  K or V swizzle cleared still reads what it wrote, but conflicts.
+  K or V swizzle cleared still reads what it wrote, but conflicts;
+- the row tiles a wave stages on its own (Q operands, the O and split-partial
+  stores) are bijections whose 16-byte writes and reads are conflict free, a
+  copy with a row-swizzle bit cleared conflicts, and 8-byte writes would
+  conflict under the dword-pass model the hardware counter supports.
 
 Reference counterpart: the swizzle offset known-answer tests of
 tests/unit/layout/test_tile_to_shape_runtime.cu:152-168 (for the NVIDIA
@@ -187,3 +191,100 @@ def test_dropped_swizzle_bit_is_detected(tmp_path, D, k_clear, v_clear):
         assert kc > 0, "a dropped K swizzle bit went unnoticed"
     if v_clear:
         assert vc > 0, "a dropped V swizzle bit went unnoticed"
+
+
+# ---- row tiles (lds::row_tile_offset) ----
+# A wave stages 32 rows of `rowb` bytes on its own: Q (rowb = 2D, 4-wave
+# workgroups) for its B operands, and on the way out O (rowb = 2D) or the
+# fp32 split partials (rowb = 128 x head-dim blocks per pass).  Every write
+# and read is 16 bytes per lane.
+
+def _row_lib(lib):
+    lib.fa_lds_row_offset.argtypes = [ctypes.c_int] * 3
+    return lib
+
+
+def _row_off(lib, r, c, rowb):
+    return lib.fa_lds_row_offset(int(r), int(c), rowb)
+
+
+@pytest.mark.parametrize("rowb", [128, 256, 512])
+def test_row_tile_is_a_bijection(lib, rowb):
+    _row_lib(lib)
+    nc = rowb // 16
+    offs = sorted(_row_off(lib, r, c, rowb) for r in range(32) for c in range(nc))
+    assert offs == list(range(0, 32 * rowb, 16))
+
+
+def _chunk_writes(lib, rowb):
+    """The output writes: ds_write_b128, lane (l32, g) writes chunk 2p + g of
+    row l32 (O after the lane-pair swap; the split partials directly)."""
+    return [[_row_off(lib, l % 32, 2 * p + l // 32, rowb) for l in range(64)]
+            for p in range(rowb // 32)]
+
+
+def _row_reads(lib, rowb):
+    """Whole-row reads: ds_read_b128, lane i reads chunk i % nc of row
+    j * (64 / nc) + i / nc."""
+    nc = rowb // 16
+    rpi = 64 // nc
+    return [[_row_off(lib, j * rpi + l // nc, l % nc, rowb) for l in range(64)]
+            for j in range(32 // rpi)]
+
+
+def _q_operand_reads(lib, rowb):
+    """Q B-operand reads: ds_read_b128, lane (l32, g) reads chunk 2kk + g of
+    row l32."""
+    return [[_row_off(lib, l % 32, 2 * kk + l // 32, rowb) for l in range(64)]
+            for kk in range(rowb // 32)]
+
+
+def _row_conflicts(lib, rowb):
+    return {
+        "writes": sum(_conflicts(a, 16, 16) for a in _chunk_writes(lib, rowb)),
+        "row_reads": sum(_conflicts(a, 16, 16) for a in _row_reads(lib, rowb)),
+        "q_reads": sum(_conflicts(a, 16, 16) for a in _q_operand_reads(lib, rowb)),
+    }
+
+
+@pytest.mark.parametrize("rowb", [128, 256, 512])
+def test_row_tile_accesses_are_bank_conflict_free(lib, rowb):
+    _row_lib(lib)
+    assert _row_conflicts(lib, rowb) == {"writes": 0, "row_reads": 0, "q_reads": 0}
+
+
+def _dword_pass_conflicts(addrs):
+    """8-byte plain accesses, served one dword at a time across all 64 lanes
+    (the model that matches the hardware counter: SQ_LDS_BANK_CONFLICT was
+    1048576 per C3 launch with 8-byte O-staging writes, whatever the swizzle,
+    and 0 with the 16-byte ones)."""
+    return sum(_conflicts([a + 4 * d for a in addrs], 4, 64) for d in range(2))
+
+
+@pytest.mark.parametrize("rowb", [128, 256])
+def test_eight_byte_output_writes_would_conflict(lib, rowb):
+    """Why O is swapped into 16-byte chunks first: writing each lane's 8-byte
+    half chunk (cols 8c + 4g .. +3 of row l32) directly puts every low dword
+    on an even bank, a 2-way conflict under any row swizzle."""
+    _row_lib(lib)
+    for c in range(rowb // 16):
+        halves = [_row_off(lib, l % 32, c, rowb) + 8 * (l // 32) for l in range(64)]
+        assert _dword_pass_conflicts(halves) > 0
+    assert all(_dword_pass_conflicts([a + 8 * (l // 32) for l, a in enumerate(w)]) > 0
+               for w in _chunk_writes(lib, rowb))
+
+
+@pytest.mark.parametrize("rowb,clear,which", [
+    (256, 8, "q_reads"),
+    (256, 1, "writes"),
+    (128, 4, "writes"),
+    (512, 8, "writes"),
+])
+def test_dropped_row_swizzle_is_detected(tmp_path, rowb, clear, which):
+    """With one row-swizzle bit cleared the tile is still a bijection but the
+    named accesses conflict."""
+    mut = _row_lib(_build(str(tmp_path), (f"FA_LDS_ROW_SWZ_CLEAR={clear}",)))
+    nc = rowb // 16
+    offs = sorted(_row_off(mut, r, c, rowb) for r in range(32) for c in range(nc))
+    assert offs == list(range(0, 32 * rowb, 16))
+    assert _row_conflicts(mut, rowb)[which] > 0
