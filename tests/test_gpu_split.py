@@ -351,22 +351,30 @@ def test_xcd_table_c5r_bitwise_equals_plain_order(fa, lib, cus):
         assert torch.equal(lse2[:, sl], lh)
 
 
-def test_causal_head_interleave_bitwise_equals_plain_order(fa):
+@pytest.mark.parametrize("B,H,N", [(1, 16, 8192), (2, 32, 2048), (4, 32, 1024)],
+                         ids=["2-heads-per-xcd", "8-heads-per-xcd", "16-heads-per-xcd"])
+def test_causal_head_interleave_bitwise_equals_plain_order(fa, B, H, N):
     """Causal grids of several rounds with B*H divisible by 8 run each XCD's
-    heads interleaved (longest q-tiles of all its heads first).  Only the
-    order changes: outputs and LSE equal, bit for bit, those of the same
-    heads run in groups of 5, 5 and 6 (not divisible by 8: plain order)."""
-    _note("case causal head interleave")
-    q, k, v = make_qkv(1, 16, 8192, 128, "bf16", seed=case_seed(960), device=DEV)
+    heads in groups of 4 (all of them when their count is not a multiple of
+    4), longest q-tiles of the group's heads first.  Only the order changes:
+    outputs and LSE equal, bit for bit, those of the same heads run in small
+    slices whose B*H is not divisible by 8 (plain order)."""
+    _note(f"case causal head interleave B{B} H{H} N{N}")
+    q, k, v = make_qkv(B, H, N, 128, "bf16", seed=case_seed(960), device=DEV)
     o, lse = fa.forward(q, k, v, causal=True, return_lse=True, split_kv=False)
     torch.cuda.synchronize()
-    for lo, hi in ((0, 5), (5, 10), (10, 16)):
+    lo = 0
+    while lo < H:
+        hi = min(H, lo + 5)
+        if (B * (hi - lo)) % 8 == 0:
+            hi -= 1
         sl = slice(lo, hi)
         ph, lh = fa.forward(q[:, sl], k[:, sl], v[:, sl], causal=True, return_lse=True,
                             split_kv=False)
         torch.cuda.synchronize()
         assert torch.equal(o[:, sl], ph), f"heads {lo}..{hi - 1}"
         assert torch.equal(lse[:, sl], lh)
+        lo = hi
 
 
 @pytest.mark.parametrize("B,H,N,D,dtype", [
