@@ -100,6 +100,7 @@ void to_kernel_args(const fa_fwd_params* p, fa::KernelArgs* a) {
   a->split.n_slots = 0;
   a->split.n_merge = 0;
   a->split.xcd_heads = 0;
+  a->split.pair = 0;
 }
 
 // Compute units of the calling thread's current device (queried once per
@@ -269,6 +270,7 @@ fa_status fa_fwd_plan(const fa_fwd_params* p, int32_t compute_units, fa_fwd_plan
   out->n_slots = a.split.n_slots;
   out->n_merge = a.split.n_merge;
   out->xcd_heads = a.split.xcd_heads;
+  out->key_halves = a.split.pair ? 2 : 1;
   for (int i = 0; i < a.split.n_items; ++i) {
     const uint32_t info = a.split.item[i];
     const int qb = (int)(info & 0xffffu), c = (int)((info >> 16) & 0xffu), nch = (int)(info >> 24);
@@ -280,7 +282,7 @@ fa_status fa_fwd_plan(const fa_fwd_params* p, int32_t compute_units, fa_fwd_plan
     out->tile_begin[i] = (int32_t)((int64_t)c * T / nch);
     out->tile_end[i] = (int32_t)((int64_t)(c + 1) * T / nch);
     const bool table = a.split.xcd_heads > 0;
-    out->slot[i] = nch > 1 ? (table ? a.split.part[i] : a.split.slot[i]) + c : -1;
+    out->slot[i] = nch > 1 ? a.split.slot[i] + c : -1;  // table items are never chunked
     out->head[i] = table ? a.split.slot[i] : -1;
   }
   return FA_OK;

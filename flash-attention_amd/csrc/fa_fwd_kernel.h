@@ -31,6 +31,7 @@ struct SplitPlan {
   int32_t n_slots;   // partial-result slots per (batch, head)
   int32_t n_merge;   // q-tiles with more than one chunk (merged by the second kernel)
   int32_t xcd_heads; // > 0: XCD placement table over this many heads per XCD
+  int32_t pair;      // 1: pair mode (8 waves per 128-row causal q-tile, no items)
   // Item i: q-tile (bits 0..15), chunk (16..23), chunk count (24..31).
   uint32_t item[kMaxSplitItems];
   // Item i's first partial slot of its q-tile (items of one q-tile use
@@ -40,9 +41,6 @@ struct SplitPlan {
   // Merge list: q-tile (bits 0..15) | chunk count (16..23), first slot in merge_slot.
   uint32_t merge[kMaxSplitItems];
   uint16_t merge_slot[kMaxSplitItems];
-  // XCD placement table: first partial slot of position i's q-tile (used
-  // when its chunk count is above 1).
-  uint16_t part[kMaxSplitItems];
 };
 
 struct KernelArgs {
@@ -78,8 +76,10 @@ int block_rows(const KernelArgs& args);
 
 // Computes the work plan for args on a device with `compute_units` CUs
 // (host code, fa_plan.cpp).
-// With allow_split it may choose split-KV and returns the workspace bytes it
-// needs; otherwise (or when no split pays) it returns 0 and leaves either no
+// Causal grids of 0.75 to 2 q-tiles per CU get pair mode (pair = 1, no
+// items, returns 0) with or without a workspace.  Otherwise, with
+// allow_split it may choose split-KV and returns the workspace bytes it
+// needs; without (or when no split pays) it returns 0 and leaves either no
 // plan (n_items = 0) or an XCD placement table (xcd_heads > 0).
 size_t plan_split(const KernelArgs& args, int compute_units, bool allow_split, SplitPlan* plan);
 

@@ -34,9 +34,14 @@
 //    clamp to the last row and the scores of keys >= N are -inf; rows >= N
 //    are never stored.
 //  * Block ids are remapped so each XCD (private L2) works on consecutive
-//    q-tiles of the same heads.  Causal grids of one round follow an XCD
-//    placement table instead (longest q-tiles alone on a CU, the others
-//    paired long with short; see plan_xcd_table).
+//    q-tiles of the same heads.  Causal 4-wave grids of exactly two q-tiles
+//    per CU follow an XCD placement table instead (q-tiles paired long with
+//    short on each CU; see plan_xcd_table).
+//  * Pair mode (causal grids of 0.75 to 2 q-tiles of 128 rows per CU): 8
+//    waves run one q-tile, waves 0-3 on the even key tiles and waves 4-7 on
+//    the odd ones, each half with its own K/V ring; the halves meet in LDS
+//    at the end.  A long q-tile then never runs as a lone 4-wave workgroup
+//    on its CU (one wave per SIMD), which set the time of such grids.
 //  * O (and the fp32 split partials) leave through LDS: each wave parks its
 //    32-row tile in the then idle K/V ring and stores whole rows, 16
 //    contiguous bytes per lane.
@@ -122,16 +127,21 @@ constexpr int kVWindow = 4;
 
 // SPLIT: the grid runs the work items of args.split (chunks of q-tiles);
 // otherwise one workgroup per q-tile.
-template <int D, bool BF16, bool CAUSAL, int NW, bool SPLIT>
+template <int D, bool BF16, bool CAUSAL, int NW, bool SPLIT, bool PAIR = false>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
     fa_fwd_kernel(const KernelArgs args) {
   using T = Tile<D>;
   using Ops = ElemOps<BF16>;
-  constexpr int BM = 32 * NW;
+  // PAIR: 8 waves on one 128-row q-tile; waves 0-3 take the even key tiles
+  // of the item, waves 4-7 the odd ones, each half with its own K/V ring,
+  // and the halves are combined through LDS at the end.
+  static_assert(!PAIR || NW == 8, "pair mode runs 8 waves");
+  constexpr int BM = PAIR ? 128 : 32 * NW;
+  constexpr int NWD = PAIR ? 4 : NW;  // waves that stage one tile
   constexpr int BN = T::BN;
   constexpr int KSTEPS = D / 16;  // MFMA k-steps for S^T (k = head dim)
   constexpr int DBLK = D / 32;    // 32-wide head-dim blocks of O^T
-  constexpr int ITERS = T::BYTES / (1024 * NW);  // DMA instructions per wave per tile
+  constexpr int ITERS = T::BYTES / (1024 * NWD);  // DMA instructions per wave per tile
   // Row sums of P in the per-tile checked pass.  O is always normalised by
   // the sum of the rounded P (the weights P V actually uses, so the weights
   // of a row sum to 1 and a dominant key's rounding cancels; with a lazy
@@ -155,12 +165,16 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
   // sum inf (or NaN), the workgroup votes, and if any row failed it recomputes
   // everything with the per-tile checked pass.  On inputs whose scores never
   // exceed the first tile's max by ~16/c in a row (e.g. the N(0, 1)
-  // benchmark inputs) the second pass never runs.
-  constexpr bool kMfmaSums = !BF16 && (!CAUSAL || NW == 8);
-  static_assert(ITERS >= 1 && T::BYTES % (1024 * NW) == 0, "tile must split evenly over waves");
+  // benchmark inputs) the second pass never runs.  Pair mode keeps the
+  // checked pass: on inputs that fail the spread test (B1 H16 N3000 with
+  // Q, K ~ N(0, 3^2)) the optimistic pass and its restart cost 9 %, more
+  // than it gains on N(0, 1) inputs (0..+8 %).
+  constexpr bool kMfmaSums = !BF16 && (!CAUSAL || (NW == 8 && !PAIR));
+  static_assert(ITERS >= 1 && T::BYTES % (1024 * NWD) == 0, "tile must split evenly over waves");
 
-  // LDS ring: K buffers 0/1 then V buffers 0/1.
-  __shared__ __attribute__((aligned(1024))) char smem[4 * T::BYTES];
+  // LDS ring: K buffers 0/1 then V buffers 0/1 (pair mode: K 0/1 of each
+  // half, then V 0/1 of each half).
+  __shared__ __attribute__((aligned(1024))) char smem[(PAIR ? 8 : 4) * T::BYTES];
   // Set by any wave whose optimistic pass left a row with a non-finite sum.
   __shared__ int redo_flag;
   if (kMfmaSums && threadIdx.x == 0) redo_flag = 0;  // ordered by the first barrier
@@ -174,6 +188,10 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
   // B4 H32 N4096).  4-wave workgroups, whose SIMD partner belongs to another
   // workgroup, raise the priority only while issuing PV MFMAs (below).
   if (NW == 8 && wave >= 4) __builtin_amdgcn_s_setprio(1);
+  const int half = PAIR ? (wave >> 2) : 0;  // key-tile half (pair mode)
+  const int rw = PAIR ? (wave & 3) : wave;   // 32-row block of the q-tile
+  const int kslot = PAIR ? 2 * half : 0;     // this half's K ring slots
+  const int vslot = PAIR ? 4 + 2 * half : 2;  // and V ring slots
   const int l32 = lane & 31;
   const int g = lane >> 5;         // which half of the wave
   const int lj = lane & 15;        // lane within its 16-lane group
@@ -236,34 +254,39 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
   const int64_t vsb = 2 * args.v_stride_s, osb = 2 * args.o_stride_s;
 
   const int q0 = qb * BM;
-  const int wrow0 = q0 + wave * 32;  // first query row of this wave
+  const int wrow0 = q0 + rw * 32;  // first query row of this wave
   const int qrow = wrow0 + l32;      // this lane's query row
   const int kv_end = CAUSAL ? min(N, q0 + BM) : N;
   const int q_tiles = (kv_end + BN - 1) / BN;  // key tiles of this q-tile
   // This item's key tiles [t_begin, t_end): chunk of n_chunks near-equal parts.
   const int t_begin = (int)((int64_t)chunk * q_tiles / n_chunks);
   const int t_end = (int)((int64_t)(chunk + 1) * q_tiles / n_chunks);
+  // This wave's tiles: t_first, t_first + TS, ... (pair mode: every other
+  // one), in n_steps steps shared by all waves of the workgroup.
+  constexpr int TS = PAIR ? 2 : 1;
+  const int t_first = t_begin + half;
+  const int n_steps = PAIR ? (t_end - t_begin + 1) / 2 : t_end - t_begin;
 
   // ---- DMA plan: per-lane 32-bit source offsets within a tile ----
   uint32_t k_src[ITERS], v_src[ITERS];
 #pragma unroll
   for (int it = 0; it < ITERS; ++it) {
     int r, c;
-    dma_slot<D, NW, false>(wave, it, lane, r, c);
+    dma_slot<D, NWD, false>(rw, it, lane, r, c);
     k_src[it] = (uint32_t)(r * ksb + c * 16);
-    dma_slot<D, NW, true>(wave, it, lane, r, c);
+    dma_slot<D, NWD, true>(rw, it, lane, r, c);
     v_src[it] = (uint32_t)(r * vsb + c * 16);
   }
   const uint32_t smem_base = __builtin_amdgcn_readfirstlane(lds_addr(smem));
-  const uint32_t wave_dma_base = smem_base + wave * ITERS * 1024;
+  const uint32_t wave_dma_base = smem_base + rw * ITERS * 1024;
 
   // Stage K and V rows [t*BN, t*BN + BN) into LDS buffer `buf`.
   auto issue_tile = [&](int t, int buf) FA_INLINE {
     const int row0 = t * BN;
     const char* kbase = kh + row0 * ksb;
     const char* vbase = vh + row0 * vsb;
-    const uint32_t kdst = wave_dma_base + buf * T::BYTES;
-    const uint32_t vdst = wave_dma_base + (2 + buf) * T::BYTES;
+    const uint32_t kdst = wave_dma_base + (kslot + buf) * T::BYTES;
+    const uint32_t vdst = wave_dma_base + (vslot + buf) * T::BYTES;
     if (row0 + BN <= N) {
 #pragma unroll
       for (int it = 0; it < ITERS; ++it) dma_16b(k_src[it], kbase, kdst + it * 1024);
@@ -273,7 +296,7 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
       // ragged tail: rows past N re-read row N-1 (their scores are masked).
       // This lane's tile row for instruction it is it*RPI + r_lane.
       constexpr int RPI = 1024 / T::ROWB;  // rows per DMA instruction
-      const int r_lane = (wave * ITERS) * RPI + lane / (T::ROWB / 16);
+      const int r_lane = (rw * ITERS) * RPI + lane / (T::ROWB / 16);
       const int last = N - 1 - row0;
 #pragma unroll
       for (int it = 0; it < ITERS; ++it) {
@@ -285,7 +308,7 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
   };
 
   // Start streaming the first tile while Q is fetched into registers.
-  issue_tile(t_begin, 0);
+  if (!PAIR || t_first < t_end) issue_tile(t_first, 0);
 
   // Q as the B operand of S^T = K Q^T: lane holds query qrow, dims
   // [16*kk + 8*g, +8) for k-step kk.  Read straight from global memory
@@ -346,7 +369,8 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
   // and halves: + 16ch + 8hf rows, as immediates).
   uint32_t v_addr[DBLK];
 #pragma unroll
-  for (int db = 0; db < DBLK; ++db) v_addr[db] = smem_base + lds::v_read_offset<D>(0, 0, db, lane);
+  for (int db = 0; db < DBLK; ++db)
+    v_addr[db] = smem_base + lds::v_read_offset<D>(0, 0, db, lane) + (vslot - 2) * T::BYTES;
 
   if constexpr (kStageQ) {
     // This wave's Q rows have landed (its own DMA): read the operands, and
@@ -369,7 +393,7 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
     constexpr bool OPT = decltype(opt_c)::value;
     static_assert(!OPT || kMfmaSums, "the optimistic pass needs the matrix-core sums");
     const int kt0 = t * BN;
-    const char* kt = smem + BUF * T::BYTES;
+    const char* kt = smem + (kslot + BUF) * T::BYTES;
 
     // ---- S^T = K Q^T : two 32-key blocks ----
     // The K operands are read kKWindow k-steps ahead of their MFMA; the
@@ -480,7 +504,7 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
     // and l are rescaled, and P is recomputed.
     bool rederive;
     if constexpr (OPT) {
-      rederive = t == t_begin;  // the first tile of every wave that computes any
+      rederive = t == t_first;  // the first tile of every wave that computes any
     } else {
       rederive = __any(!(t0 + t1 < kSumLimit));
     }
@@ -544,21 +568,22 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
 
   auto tile_step = [&](auto buf_c, int t, auto opt_c) FA_INLINE {
     constexpr int BUF = decltype(buf_c)::value;
-    if (t + 1 < t_end) issue_tile(t + 1, BUF ^ 1);
+    if (t + TS < t_end) issue_tile(t + TS, BUF ^ 1);
     // Skip tiles whose every key lies after every row of this wave.
-    if (!CAUSAL || t * BN <= wrow0 + 31) compute_tile(buf_c, t, opt_c);
+    if ((!PAIR || t < t_end) && (!CAUSAL || t * BN <= wrow0 + 31)) compute_tile(buf_c, t, opt_c);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   };
   auto run_tiles = [&](auto opt_c) FA_INLINE {
     constexpr bool OPT = decltype(opt_c)::value;
-    for (int t = t_begin; t < t_end; t += 2) {
+    for (int u = 0; u < n_steps; u += 2) {
+      const int t = t_first + TS * u;
       tile_step(std::integral_constant<int, 0>{}, t, opt_c);
       // Optimistic pass: leave it after the first tile if a wave's spread
       // test failed (the flag was set before the tile's closing barrier).
       if constexpr (OPT)
-        if (t == t_begin && __builtin_amdgcn_readfirstlane(redo_flag) != 0) break;
-      if (t + 1 < t_end) tile_step(std::integral_constant<int, 1>{}, t + 1, opt_c);
+        if (u == 0 && __builtin_amdgcn_readfirstlane(redo_flag) != 0) break;
+      if (u + 1 < n_steps) tile_step(std::integral_constant<int, 1>{}, t + TS, opt_c);
     }
   };
   // l_tot: the row sum for the LSE; lr_tot: the sum of the rounded P, which
@@ -582,7 +607,7 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
       neg_mc = INFINITY;
       l_run = 0.0f;
       lr_run = 0.0f;
-      issue_tile(t_begin, 0);
+      if (!PAIR || t_first < t_end) issue_tile(t_first, 0);
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
       run_tiles(std::false_type{});
@@ -595,6 +620,34 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
     lr_tot = kUnroundedSum ? pair_sum(lr_run) : l_tot;
   }
 
+  if constexpr (PAIR) {
+    // Combine the halves: waves 4-7 hand O (unnormalised), the offset m and
+    // the sums to their row partners through LDS, above the rows the
+    // epilogue stages; each half's terms are rescaled to the larger offset.
+    constexpr int XO = DBLK * 16 * 64;  // floats of O per wave
+    float* xo = reinterpret_cast<float*>(smem + 256 * D) + rw * (XO + 4 * 64);
+    float* xm = xo + XO;
+    if (half == 1) {
+#pragma unroll
+      for (int db = 0; db < DBLK; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) xo[(db * 16 + i) * 64 + lane] = o_acc[db][i];
+      *reinterpret_cast<f32x4*>(xm + 4 * lane) = f32x4{m_run, l_tot, lr_tot, 0.0f};
+    }
+    __syncthreads();
+    if (half == 1) return;
+    const f32x4 o1 = *reinterpret_cast<const f32x4*>(xm + 4 * lane);
+    const float m = fmaxf(m_run, o1[0]);
+    const float a0 = m_run == -INFINITY ? 0.0f : fast_exp2((m_run - m) * c);
+    const float a1 = o1[0] == -INFINITY ? 0.0f : fast_exp2((o1[0] - m) * c);
+#pragma unroll
+    for (int db = 0; db < DBLK; ++db)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) o_acc[db][i] = o_acc[db][i] * a0 + xo[(db * 16 + i) * 64 + lane] * a1;
+    l_tot = l_tot * a0 + o1[1] * a1;
+    lr_tot = lr_tot * a0 + o1[2] * a1;
+    m_run = m;
+  }
   const bool row_ok = qrow < N;
   // The output goes out through LDS, whole rows at a time.  In the O^T
   // accumulator a lane holds 4 consecutive head dims of one row per (db, r),
@@ -632,7 +685,7 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
     // when no key of this chunk is visible to the row), the row sum l for the
     // LSE and the sum of the rounded P for the normalisation ----
     const int64_t slot =
-        (int64_t)(args.split.xcd_heads > 0 ? args.split.part[item] : args.split.slot[item]) + chunk;
+        (int64_t)args.split.slot[item] + chunk;  // (table items are never chunked)
     const int64_t row0 = ((int64_t)bh * args.split.n_slots + slot) * BM + (wrow0 - q0);
     // fp32 rows of 4D bytes: NW / 4 passes of DBLK / (NW / 4) head-dim
     // blocks each fit the ring (NW x 32 x 4D / passes <= 4 x 64 x 2D).
@@ -766,10 +819,12 @@ __global__ void __launch_bounds__(256) fa_merge_kernel(const KernelArgs args, in
     args.lse[(int64_t)bh * args.seq_len + q] = (m == -INFINITY ? 0.0f : m) * args.scale + __logf(l);
 }
 
-template <int D, bool BF16, bool CAUSAL, int NW>
+template <int D, bool BF16, bool CAUSAL, int NW, bool PAIR = false>
 hipError_t launch_one(const KernelArgs& a, hipStream_t stream) {
-  constexpr int BM = 32 * NW;
+  constexpr int BM = PAIR ? 128 : 32 * NW;
   KernelArgs args = a;
+  // Pair mode runs one workgroup per q-tile, longest first; its plan has no items.
+  if (PAIR && (a.split.n_items != 0 || !CAUSAL)) return hipErrorInvalidValue;
   args.n_qblocks = (args.seq_len + BM - 1) / BM;
   // A plan is only valid for the block height it was made for; partials
   // need the workspace; a placement table covers 8 XCDs of whole heads.
@@ -788,19 +843,23 @@ hipError_t launch_one(const KernelArgs& a, hipStream_t stream) {
   // HIP call by the caller is not reported as (or lost to) this launch.
   void* kargs[] = {&args};
   if (args.split.n_items == 0)
-    return hipLaunchKernel(reinterpret_cast<const void*>(&fa_fwd_kernel<D, BF16, CAUSAL, NW, false>),
+    return hipLaunchKernel(reinterpret_cast<const void*>(&fa_fwd_kernel<D, BF16, CAUSAL, NW, false, PAIR>),
                            dim3((unsigned)total), dim3(NW * 64), kargs, 0, stream);
-  hipError_t e =
-      hipLaunchKernel(reinterpret_cast<const void*>(&fa_fwd_kernel<D, BF16, CAUSAL, NW, true>),
-                      dim3((unsigned)total), dim3(NW * 64), kargs, 0, stream);
-  if (e != hipSuccess || sp.n_merge == 0) return e;
-  constexpr int RPB = 256 / (D / 4);
-  const int64_t merge_blocks = bh * args.split.n_merge * ((BM + RPB - 1) / RPB);
-  if (merge_blocks > 0x7fffffff) return hipErrorInvalidValue;
-  int bm = BM;
-  void* margs[] = {&args, &bm};
-  return hipLaunchKernel(reinterpret_cast<const void*>(&fa_merge_kernel<D, BF16>),
-                         dim3((unsigned)merge_blocks), dim3(256), margs, 0, stream);
+  if constexpr (PAIR) {
+    return hipErrorInvalidValue;  // (rejected above: pair plans have no items)
+  } else {
+    hipError_t e =
+        hipLaunchKernel(reinterpret_cast<const void*>(&fa_fwd_kernel<D, BF16, CAUSAL, NW, true>),
+                        dim3((unsigned)total), dim3(NW * 64), kargs, 0, stream);
+    if (e != hipSuccess || sp.n_merge == 0) return e;
+    constexpr int RPB = 256 / (D / 4);
+    const int64_t merge_blocks = bh * args.split.n_merge * ((BM + RPB - 1) / RPB);
+    if (merge_blocks > 0x7fffffff) return hipErrorInvalidValue;
+    int bm = BM;
+    void* margs[] = {&args, &bm};
+    return hipLaunchKernel(reinterpret_cast<const void*>(&fa_merge_kernel<D, BF16>),
+                           dim3((unsigned)merge_blocks), dim3(256), margs, 0, stream);
+  }
 }
 
 template <int D, bool BF16>
@@ -811,6 +870,8 @@ hipError_t launch_causal(const KernelArgs& a, hipStream_t stream) {
     // and short problems lose (-11 % at N = 3000: fewer, longer workgroups).
     if constexpr (!BF16)
       if (a.seq_len >= kWideCausalMinSeq) return launch_one<D, BF16, true, 8>(a, stream);
+    // Grids of 0.75 to 2 q-tiles per CU: pair mode (plan_split decides).
+    if (a.split.pair) return launch_one<D, BF16, true, 8, true>(a, stream);
     return launch_one<D, BF16, true, 4>(a, stream);
   }
   // Long non-causal rows: 8 waves (BM = 256) per workgroup, one workgroup

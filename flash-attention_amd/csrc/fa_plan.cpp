@@ -112,16 +112,11 @@ size_t plan_chunks(const KernelArgs& a, int compute_units, SplitPlan* plan) {
 // longest: at B1 H16 N3000 the 47-tile q-tile shared its CU with a 32-tile
 // one and set the kernel time (66 us).  The table gives the alone
 // positions the longest items and pairs the rest longest with shortest.
-//
-// With allow_split the longest k q-tiles of every head may also be cut in
-// two chunks, as long as the grid stays one round (n + k * heads_per_xcd
-// <= 2 cpx); k is chosen by a model of the round: a workgroup alone costs
-// 1 per key tile, two sharing a CU 1.85 each while both run (measured
-// 1.14 us and 2.1 us per 128x64 tile), 1.5 per workgroup for its prologue,
-// and a split adds the merge (about 3.5 tile times plus the partials'
-// fp32 read-back at ~4 TB/s).  Returns the workspace bytes (0 unsplit).
-size_t plan_xcd_table(const KernelArgs& a, int compute_units, bool allow_split,
-                      SplitPlan* plan) {
+// Grids of 0.75 to 2 q-tiles per CU run in pair mode (plan_split), so the
+// table remains for n = 2 cpx, where no CU runs alone and the pairing is
+// the whole gain.  No q-tile is split and the kernel's arithmetic is that
+// of the plain grid (only the order changes).  Returns 0 (no workspace).
+size_t plan_xcd_table(const KernelArgs& a, int compute_units, SplitPlan* plan) {
   const int BM = block_rows(a);
   if (!a.causal || BM != 128 || compute_units % 8 != 0) return 0;
   const int64_t bh = (int64_t)a.batch * a.heads;
@@ -129,97 +124,64 @@ size_t plan_xcd_table(const KernelArgs& a, int compute_units, bool allow_split,
   const int nq = (a.seq_len + BM - 1) / BM;
   const int64_t hpx = bh / 8;
   const int64_t cpx = compute_units / 8;
-  const int64_t n0 = hpx * nq;
-  if (n0 <= cpx || n0 > 2 * cpx || n0 > kMaxSplitItems) return 0;
-  const int k_max =
-      allow_split ? (int)std::min<int64_t>(nq, (std::min<int64_t>(2 * cpx, kMaxSplitItems) - n0) / hpx)
-                  : 0;
-  constexpr double kShared = 2.1 / 1.14, kPrologue = 1.5, kMergeFixed = 3.5;
-  const double tile_us = a.head_dim == 128 ? 1.14 : 0.62;
-  struct Entry { int len, qb, head, c, nch; };
+  const int64_t n = hpx * nq;
+  if (n <= cpx || n > 2 * cpx || n > kMaxSplitItems) return 0;
+  struct Entry { int len, qb, head; };
   Entry all[kMaxSplitItems];
-  auto build = [&](int k) {  // the k longest q-tiles (the last k) of every head in two chunks
-    int cnt = 0;
-    for (int h = 0; h < (int)hpx; ++h)
-      for (int qb = 0; qb < nq; ++qb) {
-        const int T = q_tile_tiles(a, BM, qb);
-        const int nch = qb >= nq - k ? 2 : 1;
-        for (int c = 0; c < nch; ++c) {
-          const int len = (int)((int64_t)(c + 1) * T / nch) - (int)((int64_t)c * T / nch);
-          all[cnt++] = Entry{len, qb, h, c, nch};
-        }
-      }
-    std::stable_sort(all, all + cnt, [](const Entry& x, const Entry& y) {
-      return x.len != y.len ? x.len > y.len : (x.qb != y.qb ? x.qb > y.qb : x.c < y.c);
-    });
-    return cnt;
-  };
-  // Position of sorted entry src for n entries: alone positions take the
+  int cnt = 0;
+  for (int h = 0; h < (int)hpx; ++h)
+    for (int qb = 0; qb < nq; ++qb) all[cnt++] = Entry{q_tile_tiles(a, BM, qb), qb, h};
+  std::stable_sort(all, all + cnt, [](const Entry& x, const Entry& y) {
+    return x.len != y.len ? x.len > y.len : x.qb > y.qb;
+  });
+  // Sorted entry src goes to position: the alone positions take the
   // longest, then pairs longest-with-shortest.
-  auto position_of = [&](int n, int src) {
-    const int m = (int)(n - cpx) > 0 ? (int)(n - cpx) : 0;
-    const int alone = (int)cpx - m;
-    if (src < alone) return m + src;
-    if (src < alone + m) return src - alone;
-    return (int)cpx + (n - 1 - src);
-  };
-  auto model = [&](int k) {
-    const int n = build(k);
-    const int m = n > cpx ? n - (int)cpx : 0;
-    const int alone = (int)cpx - m;
-    double worst = 0.0;
-    for (int i = 0; i < alone && i < n; ++i) worst = std::max(worst, all[i].len + kPrologue);
-    for (int j = 0; j < m; ++j) {
-      const double x = all[alone + j].len + kPrologue, y = all[n - 1 - j].len + kPrologue;
-      worst = std::max(worst, std::min(x, y) * kShared + std::fabs(x - y));
-    }
-    if (k > 0) {
-      const double bytes = (double)bh * 2 * k * BM * ((double)a.head_dim * 4 + 16);
-      worst += kMergeFixed * 1.14 / tile_us + bytes / 4e12 / (tile_us * 1e-6);
-    }
-    return worst;
-  };
-  int best_k = 0;
-  double best = model(0);
-  for (int k = 1; k <= k_max; ++k) {
-    const double c = model(k);
-    if (c < best - 1e-9) {
-      best = c;
-      best_k = k;
-    }
+  const int m = (int)(n - cpx);
+  const int alone = (int)cpx - m;
+  for (int src = 0; src < cnt; ++src) {
+    const int pos = src < alone ? m + src : (src < alone + m ? src - alone : (int)cpx + (cnt - 1 - src));
+    plan->item[pos] = (uint32_t)all[src].qb | (1u << 24);
+    plan->slot[pos] = (uint16_t)all[src].head;
   }
-  const int n = build(best_k);
-  for (int src = 0; src < n; ++src) {
-    const int pos = position_of(n, src);
-    const Entry& e = all[src];
-    plan->item[pos] = (uint32_t)e.qb | ((uint32_t)e.c << 16) | ((uint32_t)e.nch << 24);
-    plan->slot[pos] = (uint16_t)e.head;
-    // partial slots: 2 per split q-tile, in q-tile order (same for every head)
-    plan->part[pos] = (uint16_t)(e.nch > 1 ? 2 * (e.qb - (nq - best_k)) : 0);
-  }
-  plan->n_items = n;
+  plan->n_items = cnt;
   plan->xcd_heads = (int)hpx;
-  if (best_k == 0) return 0;
-  for (int j = 0; j < best_k; ++j) {
-    plan->merge[j] = (uint32_t)(nq - best_k + j) | (2u << 16);
-    plan->merge_slot[j] = (uint16_t)(2 * j);
-  }
-  plan->n_merge = best_k;
-  plan->n_slots = 2 * best_k;
-  return (size_t)bh * plan->n_slots * BM * ((size_t)a.head_dim * 4 + 16);
+  return 0;
 }
 
 }  // namespace
 
+// Pair mode for causal 4-wave grids of 0.75 to 2 q-tiles (128 rows) per CU:
+// one 8-wave workgroup per q-tile, its halves on alternate key tiles, one
+// workgroup per CU, dispatched longest first.  Such grids are bound by
+// their longest q-tiles, which a 4-wave workgroup runs alone on its CU
+// once its partner is done (1.55 us per key tile alone against 2.1 us for
+// each of two sharing it, at B1 H16 N3000); a pair workgroup keeps two waves
+// on every SIMD.  Measured against the 4-wave kernel with its plans: +7..8 %
+// at B1 H16 N3000 (Q, K ~ N(0, 3^2)), +8..27 % at H8..H16 N2048..6000
+// (bf16 and D = 64 included); -6..-12 % at H24 and H32 N3000 (2.25 and 3 per
+// CU) and -20..-49 % below 0.75 per CU (H4, H6), where split-KV spreads the
+// few long q-tiles over more CUs.
+namespace {
+bool pair_mode(const KernelArgs& a, int compute_units) {
+  if (!a.causal || block_rows(a) != 128) return false;
+  const int64_t items = (int64_t)a.batch * a.heads * ((a.seq_len + 127) / 128);
+  return 4 * items >= 3 * (int64_t)compute_units && items < 2 * (int64_t)compute_units;
+}
+}  // namespace
+
 size_t plan_split(const KernelArgs& a, int compute_units, bool allow_split, SplitPlan* plan) {
-  plan->n_items = plan->n_slots = plan->n_merge = plan->xcd_heads = 0;
+  plan->n_items = plan->n_slots = plan->n_merge = plan->xcd_heads = plan->pair = 0;
   if (compute_units < 1) return 0;
+  if (pair_mode(a, compute_units)) {
+    plan->pair = 1;
+    return 0;
+  }
   if (allow_split) {
     const size_t bytes = plan_chunks(a, compute_units, plan);
     if (bytes > 0) return bytes;
     plan->n_items = plan->n_slots = plan->n_merge = 0;
   }
-  return plan_xcd_table(a, compute_units, allow_split, plan);
+  return plan_xcd_table(a, compute_units, plan);
 }
 
 }  // namespace fa

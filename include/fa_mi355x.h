@@ -120,7 +120,8 @@ typedef struct {
   int32_t reserved;
 } fa_device_info_t;
 
-/* Split-KV plan of a problem (diagnostic; filled by fa_fwd_plan). */
+/* Work plan of a problem (diagnostic; filled by fa_fwd_plan): split-KV, an XCD
+ * placement table, pair mode, or none. */
 #define FA_PLAN_MAX_ITEMS 128
 typedef struct {
   int32_t block_rows;       /* query rows per workgroup (q-tile height) of the kernel */
@@ -128,6 +129,8 @@ typedef struct {
   int32_t n_slots;          /* partial-result slots per (batch, head) in the workspace */
   int32_t n_merge;          /* q-tiles with more than one chunk (merged by a second kernel) */
   int32_t xcd_heads;        /* > 0: XCD placement table (no split) over this many heads per XCD */
+  int32_t key_halves;       /* 2: pair mode (8 waves per q-tile, each half on alternate key
+                               tiles, one workgroup per q-tile, no items); 1 otherwise */
   uint64_t workspace_bytes; /* bytes fa_fwd_ws needs (0 when unsplit) */
   /* Split-KV (xcd_heads == 0): work item i (dispatch order, longest first)
    * of every (batch, head) is q-tile q_tile[i], key tiles (64 keys each)
@@ -194,7 +197,7 @@ fa_status fa_fwd_ws_timed(const fa_fwd_params* p, void* workspace, uint64_t work
 fa_status fa_fwd_scratch(const fa_fwd_params* p, void* stream);
 
 /* The work plan fa_fwd_ws would use for *p on a device with
- * `compute_units` CUs (split-KV, or an XCD placement table, or none).
+ * `compute_units` CUs (split-KV, an XCD placement table, pair mode, or none).
  * Host only; touches no GPU. */
 fa_status fa_fwd_plan(const fa_fwd_params* p, int32_t compute_units, fa_fwd_plan_t* out);
 

@@ -113,7 +113,8 @@ int main(void) {
   F(fa_device_info_t, max_threads_per_block); F(fa_device_info_t, wavefront_size);
   F(fa_device_info_t, arch_major); F(fa_device_info_t, arch_minor); F(fa_device_info_t, reserved);
   F(fa_fwd_plan_t, block_rows); F(fa_fwd_plan_t, n_items); F(fa_fwd_plan_t, n_slots);
-  F(fa_fwd_plan_t, n_merge); F(fa_fwd_plan_t, xcd_heads); F(fa_fwd_plan_t, workspace_bytes);
+  F(fa_fwd_plan_t, n_merge); F(fa_fwd_plan_t, xcd_heads); F(fa_fwd_plan_t, key_halves);
+  F(fa_fwd_plan_t, workspace_bytes);
   F(fa_fwd_plan_t, q_tile); F(fa_fwd_plan_t, tile_begin); F(fa_fwd_plan_t, tile_end);
   F(fa_fwd_plan_t, n_chunks); F(fa_fwd_plan_t, slot); F(fa_fwd_plan_t, head);
   printf("\"sizeof.fa_fwd_params\": [%zu, 0], \"sizeof.fa_device_info_t\": [%zu, 0], "

@@ -1,6 +1,6 @@
 """Seeded random problems aimed at each work plan of the forward: plain
-grids, bound-driven split-KV, and XCD placement tables with and without
-chunks.  Each case records the plan the library chose for this device and
+grids, bound-driven split-KV, and one-round causal grids (pair mode, or the
+XCD placement table at exactly two q-tiles per CU).  Each case records the plan the library chose for this device and
 checks the result on sampled rows against the fp64 oracle and the
 reference-kernel emulator (2x bars as in test_gpu_parity.py for random
 problems), and against the one-workgroup-per-q-tile result (split_kv=False)
@@ -40,7 +40,7 @@ def _draw(case):
     elif kind == 1:  # bound-driven split: few heads, long rows
         B, H = 1, int(rng.integers(1, 5))
         N, causal = int(rng.integers(1500, 6000)), bool(rng.integers(0, 2))
-    else:  # XCD placement table: whole heads per XCD, one round of 4-wave workgroups
+    else:  # one round of 4-wave workgroups: pair mode (or the XCD placement table)
         hpx = int(rng.integers(1, 5))
         nq = int(rng.integers(32 // hpx + 1, 64 // hpx + 1))
         N = int(rng.integers((nq - 1) * 128 + 1, nq * 128 + 1))
@@ -68,14 +68,14 @@ def test_random_plans_vs_oracle(fa, oracle, lib, case):
     p = A.params_from_tensors(q, k, v, torch.empty_like(q), None, causal)
     pl = A.FaFwdPlan()
     assert lib.fa_fwd_plan(ctypes.byref(p), cus, ctypes.byref(pl)) == A.FA_OK
-    kind = ("table+chunks" if pl.xcd_heads and pl.n_merge else "table" if pl.xcd_heads
+    kind = ("pair" if pl.key_halves == 2 else "table" if pl.xcd_heads
             else "split" if pl.n_items else "plain")
     _note(f"case {case}: {B}x{H}x{N}x{D} {dtype} causal={causal} sigma={sigma} plan={kind}")
     o, lse = fa.forward(q, k, v, causal=causal, return_lse=True)
     o1, lse1 = fa.forward(q, k, v, causal=causal, return_lse=True, split_kv=False)
     torch.cuda.synchronize()
     assert torch.isfinite(o).all().item()
-    if kind in ("plain", "table"):
+    if kind in ("plain", "table", "pair"):
         assert torch.equal(o, o1) and torch.equal(lse, lse1)
     else:
         _vs_unsplit(o, lse, o1, lse1, dtype)

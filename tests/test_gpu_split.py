@@ -132,13 +132,13 @@ def test_split_softmax_scale_vs_oracle(fa, oracle, lib, cus, scale):
     _check_against_oracle(oracle, q, k, v, o, lse, True, scale, "fp16", contract=False)
 
 
-def test_split_c5r_half_heads_vs_oracle_and_unsplit(fa, oracle, lib, cus):
-    """C5r's shape and inputs (N3000 causal fp16, Q, K ~ N(0, 3^2)) with 8 of
-    its 16 heads, which the plan splits into up to 5 chunks per q-tile:
+def test_split_c5r_quarter_heads_vs_oracle_and_unsplit(fa, oracle, lib, cus):
+    """C5r's shape and inputs (N3000 causal fp16, Q, K ~ N(0, 3^2)) with 4 of
+    its 16 heads, which the plan splits into up to 3 chunks per q-tile:
     sampled rows against the oracle and the reference-kernel emulator, and
     split == unsplit within two roundings."""
-    _note("case split C5r/2")
-    B, H, N, D = 1, 8, 3000, 128
+    _note("case split C5r/4")
+    B, H, N, D = 1, 4, 3000, 128
     q, k, v = make_qkv(B, H, N, D, "fp16", seed=case_seed(5), qk_sigma=3.0, device=DEV)
     pl = _assert_split(lib, cus, q, k, v, True)
     assert pl.block_rows == 128
@@ -321,51 +321,53 @@ def test_abi_unsplit_problem_needs_no_workspace(fa, lib):
     assert torch.equal(o, fa.forward(q, k, v, causal=causal))
 
 
-def test_xcd_table_c5r_bitwise_equals_plain_order(fa, lib, cus):
-    """C5r runs with the XCD placement table.  Without a workspace
-    (split_kv=False) the table is a dispatch order only: every head's output
-    and LSE are bit for bit those of the same heads run in the plain
-    longest-first order (4 heads per call, no table, no split).  With the
-    default workspace the table also cuts the longest q-tiles in two
-    chunks: equal to the unsplit result within the split-KV bounds (its
-    rows against the oracle: test_config_sampled_rows_vs_oracle)."""
-    _note("case XCD table C5r")
+def _assert_pair(lib, cus, q, k, v):
+    pl = _plan(lib, cus, q, k, v, torch.empty_like(q), True)
+    _note(f"  plan: key_halves={pl.key_halves} items={pl.n_items} xcd_heads={pl.xcd_heads}")
+    assert pl.key_halves == 2 and pl.n_items == 0 and pl.workspace_bytes == 0
+    return pl
+
+
+def test_pair_mode_c5r_order_and_workspace_invariance(fa, lib, cus):
+    """C5r runs in pair mode (rows against the oracle: the full-tensor config
+    test).  Each q-tile is computed by one workgroup whatever its position in
+    the grid, and the workspace is not used: the result with a workspace
+    equals the one without, and permuting the heads permutes the output and
+    LSE, bit for bit."""
+    _note("case pair mode C5r")
     q, k, v, causal, _ = make_config("C5r", device=DEV)
-    pl = _plan(lib, cus, q, k, v, torch.empty_like(q), causal)
-    _note(f"  plan: xcd_heads={pl.xcd_heads} items={pl.n_items} merge={pl.n_merge}")
     if cus == 256:
-        assert pl.xcd_heads == 2 and pl.n_items == 64 and pl.n_merge == 8
+        _assert_pair(lib, cus, q, k, v)
     o, lse = fa.forward(q, k, v, causal=True, return_lse=True)
     o2, lse2 = fa.forward(q, k, v, causal=True, return_lse=True, split_kv=False)
     torch.cuda.synchronize()
     assert torch.isfinite(o).all().item()
-    _vs_unsplit(o, lse, o2, lse2, "fp16")
-    for h in range(0, q.shape[1], 4):
-        sl = slice(h, h + 4)
-        p4 = _plan(lib, cus, q[:, sl], k[:, sl], v[:, sl], torch.empty_like(q[:, sl]), causal)
-        assert p4.xcd_heads == 0
-        ph, lh = fa.forward(q[:, sl], k[:, sl], v[:, sl], causal=True, return_lse=True,
-                            split_kv=False)
-        torch.cuda.synchronize()
-        assert torch.equal(o2[:, sl], ph), f"heads {h}..{h + 3}"
-        assert torch.equal(lse2[:, sl], lh)
+    assert torch.equal(o, o2) and torch.equal(lse, lse2)
+    perm = torch.tensor([5, 12, 0, 9, 3, 15, 7, 1, 10, 14, 2, 8, 13, 4, 11, 6], device=DEV)
+    qp, kp, vp = (t[:, perm].contiguous() for t in (q, k, v))
+    op, lp = fa.forward(qp, kp, vp, causal=True, return_lse=True)
+    torch.cuda.synchronize()
+    assert torch.equal(op, o[:, perm]) and torch.equal(lp, lse[:, perm])
 
 
 @pytest.mark.parametrize("B,H,N", [(1, 16, 8192), (2, 32, 2048), (4, 32, 1024)],
                          ids=["2-heads-per-xcd", "8-heads-per-xcd", "16-heads-per-xcd"])
-def test_causal_head_interleave_bitwise_equals_plain_order(fa, B, H, N):
+def test_causal_head_interleave_bitwise_equals_plain_order(fa, cus, B, H, N):
     """Causal grids of several rounds with B*H divisible by 8 run each XCD's
     heads in groups of 4 (all of them when their count is not a multiple of
     4), longest q-tiles of the group's heads first.  Only the order changes:
     outputs and LSE equal, bit for bit, those of the same heads run in small
-    slices whose B*H is not divisible by 8 (plain order)."""
+    slices whose B*H is not divisible by 8 (plain order), and small enough
+    (below 0.75 q-tiles per CU) not to run in pair mode."""
     _note(f"case causal head interleave B{B} H{H} N{N}")
     q, k, v = make_qkv(B, H, N, 128, "bf16", seed=case_seed(960), device=DEV)
     o, lse = fa.forward(q, k, v, causal=True, return_lse=True, split_kv=False)
     torch.cuda.synchronize()
+    nq = (N + 127) // 128
+    width = max(w for w in range(1, 6) if 4 * B * w * nq < 3 * cus and (B * w) % 8 != 0)
     lo = 0
     while lo < H:
-        hi = min(H, lo + 5)
+        hi = min(H, lo + width)
         if (B * (hi - lo)) % 8 == 0:
             hi -= 1
         sl = slice(lo, hi)
@@ -377,36 +379,10 @@ def test_causal_head_interleave_bitwise_equals_plain_order(fa, B, H, N):
         lo = hi
 
 
-@pytest.mark.parametrize("B,H,N,D,dtype", [
-    (1, 16, 2200, 64, "bf16"),   # table, 11 q-tiles per head in two chunks
-    (2, 8, 3001, 128, "fp16"),   # table with chunks, ragged, two batches
-    (1, 24, 1500, 64, "fp16"),   # table over 3 heads per XCD, no chunks
-    (2, 16, 1300, 128, "bf16"),  # table over 4 heads per XCD, no chunks
-])
-def test_xcd_table_variants_vs_oracle(fa, oracle, lib, cus, B, H, N, D, dtype):
-    """XCD placement tables with and without chunks, D = 64 and 128, fp16
-    and bf16, ragged N, several heads per XCD: sampled rows against the
-    oracle and the reference-kernel emulator; the default (workspace) path
-    against split_kv=False within the split-KV bounds; and split_kv=False
-    (table order only) bit for bit against the plain order, computed one
-    batch and head at a time."""
-    _note(f"case XCD table {B}x{H}x{N}x{D} {dtype}")
-    q, k, v = make_qkv(B, H, N, D, dtype, seed=case_seed(970 + N), device=DEV)
-    pl = _plan(lib, cus, q, k, v, torch.empty_like(q), True)
-    _note(f"  plan: xcd_heads={pl.xcd_heads} items={pl.n_items} merge={pl.n_merge}")
-    if cus == 256:
-        assert pl.xcd_heads == B * H // 8
-    o, lse, o1, lse1 = _both(fa, q, k, v, True)
-    _vs_unsplit(o, lse, o1, lse1, dtype)
-    for b in range(B):
-        for h in (0, H // 2, H - 1):
-            ph, lh = fa.forward(q[b:b + 1, h:h + 1], k[b:b + 1, h:h + 1], v[b:b + 1, h:h + 1],
-                                causal=True, return_lse=True, split_kv=False)
-            torch.cuda.synchronize()
-            assert torch.equal(o1[b:b + 1, h:h + 1], ph), (b, h)
-            assert torch.equal(lse1[b:b + 1, h:h + 1], lh), (b, h)
-    rng = np.random.default_rng(970)
-    heads, sel_bh, sel_row = _sample_rows(N, B * H, rng, n_random=24)
+def _sampled_rows_vs_oracle(oracle, q, k, v, o, lse, dtype, seed, n_random=24):
+    B, H, N, D = q.shape
+    rng = np.random.default_rng(seed)
+    heads, sel_bh, sel_row = _sample_rows(N, B * H, rng, n_random=n_random)
     qn, kn, vn = (to_np32(t.reshape(1, B * H, N, D)) for t in (q, k, v))
     scale = 1.0 / math.sqrt(D)
     ref_o, ref_lse = oracle.attn_rows_f64(qn, kn, vn, scale, True, sel_bh, sel_row)
@@ -424,11 +400,75 @@ def test_xcd_table_variants_vs_oracle(fa, oracle, lib, cus, B, H, N, D, dtype):
     assert lse_err <= LSE_TOL
 
 
-def test_abi_fa_fwd_table_graph_capture(fa, lib, cus):
-    """fa_fwd (no workspace) with C5r's XCD placement table, called through
-    the raw C ABI inside a captured HIP graph: every replay equals the eager
-    result, with eager launches in between."""
-    _note("case C ABI table graph capture")
+@pytest.mark.parametrize("B,H,N,D,dtype,sigma", [
+    (1, 16, 2200, 64, "bf16", 1.0),   # 288 q-tiles
+    (2, 8, 3001, 128, "fp16", 1.0),   # ragged, two batches
+    (1, 24, 1500, 64, "fp16", 3.0),   # H not a multiple of 8, peaked rows
+    (2, 16, 1300, 128, "bf16", 1.0),
+    (1, 8, 3000, 128, "fp16", 3.0),   # 192 q-tiles: the lower end of the range
+])
+def test_pair_mode_variants_vs_oracle(fa, oracle, lib, cus, B, H, N, D, dtype, sigma):
+    """Pair mode at D = 64 and 128, fp16 and bf16, ragged N, several batches:
+    sampled rows against the oracle and the reference-kernel emulator; with
+    and without a workspace bit for bit (one kernel); and against the same
+    heads computed one batch and head at a time (4-wave workgroups, no pair
+    mode) within the split-KV bounds (the halves' offsets differ, so P
+    rounds differently, and the halves meet in fp32)."""
+    _note(f"case pair mode {B}x{H}x{N}x{D} {dtype} sigma={sigma}")
+    q, k, v = make_qkv(B, H, N, D, dtype, seed=case_seed(970 + N), qk_sigma=sigma, device=DEV)
+    if cus == 256:
+        _assert_pair(lib, cus, q, k, v)
+    o, lse, o1, lse1 = _both(fa, q, k, v, True)
+    assert torch.equal(o, o1) and torch.equal(lse, lse1)
+    for b in range(B):
+        for h in (0, H // 2, H - 1):
+            sl = (slice(b, b + 1), slice(h, h + 1))
+            ph, lh = fa.forward(q[sl], k[sl], v[sl], causal=True, return_lse=True,
+                                split_kv=False)
+            torch.cuda.synchronize()
+            _vs_unsplit(o[sl], lse[sl], ph, lh, dtype)
+    _sampled_rows_vs_oracle(oracle, q, k, v, o, lse, dtype, 970)
+
+
+@pytest.mark.parametrize("B,H,N,D,dtype", [
+    (4, 16, 1000, 64, "bf16"),   # 8 heads x 8 q-tiles per XCD
+    (2, 32, 1024, 128, "fp16"),
+])
+def test_xcd_table_vs_oracle_and_plain_order(fa, oracle, lib, cus, B, H, N, D, dtype):
+    """Grids of exactly two q-tiles per CU run with the XCD placement table:
+    a dispatch order only, so the output and LSE equal, bit for bit, those of
+    the same heads in the plain longest-first order (slices of heads whose
+    B*H is not a multiple of 8 get no table); sampled rows against the oracle
+    and the reference-kernel emulator."""
+    _note(f"case XCD table {B}x{H}x{N}x{D} {dtype}")
+    q, k, v = make_qkv(B, H, N, D, dtype, seed=case_seed(980 + N), device=DEV)
+    pl = _plan(lib, cus, q, k, v, torch.empty_like(q), True)
+    _note(f"  plan: xcd_heads={pl.xcd_heads} items={pl.n_items} merge={pl.n_merge}")
+    if cus == 256:
+        assert pl.xcd_heads == B * H // 8 and pl.n_items == 64 and pl.n_merge == 0
+    o, lse, o1, lse1 = _both(fa, q, k, v, True)
+    assert torch.equal(o, o1) and torch.equal(lse, lse1)
+    for lo in range(0, H, 5):
+        hi = min(H, lo + 5)
+        if (B * (hi - lo)) % 8 == 0:
+            hi -= 1
+        for hh in ((lo, hi), (hi, min(H, hi + 1))):
+            if hh[0] >= hh[1]:
+                continue
+            sl = slice(*hh)
+            ph, lh = fa.forward(q[:, sl], k[:, sl], v[:, sl], causal=True, return_lse=True,
+                                split_kv=False)
+            torch.cuda.synchronize()
+            assert torch.equal(o1[:, sl], ph), f"heads {hh}"
+            assert torch.equal(lse1[:, sl], lh)
+    _sampled_rows_vs_oracle(oracle, q, k, v, o, lse, dtype, 980)
+
+
+def test_abi_fa_fwd_pair_graph_capture(fa, lib, cus):
+    """fa_fwd (no workspace) on C5r (pair mode), called through the raw C
+    ABI inside a captured HIP graph: every replay equals the eager result,
+    with eager launches in between."""
+    _note("case C ABI pair mode graph capture")
     q, k, v, causal, _ = make_config("C5r", device=DEV)
     o = torch.empty_like(q)
     p = A.params_from_tensors(q, k, v, o, None, causal)

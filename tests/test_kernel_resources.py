@@ -3,7 +3,8 @@ assembly that hipcc emits for csrc/fa_fwd_kernel.hip with the library's own
 flags (CPU only: hipcc cross-compiles without a GPU).
 
 - Every forward variant fits two waves per SIMD (at most 256 VGPRs, no
-  AGPRs), with no scratch and no VGPR spills.
+  AGPRs), with no scratch and no VGPR spills; the pair-mode variants hold two
+  K/V rings (128 KiB at D = 128, one workgroup per CU).
 - m0 discipline of the K/V staging: the DMA is issued from inline asm that
   sets m0 (the LDS destination) immediately before each
   global_load_lds_dwordx4 and declares m0 clobbered.  The compiler does not
@@ -58,7 +59,14 @@ def _kernel_metadata(asm: str):
 def test_forward_variants_fit_two_waves_per_simd(device_asm):
     kernels = _kernel_metadata(device_asm)
     fwd = [(n, f) for n, f in kernels if "fa_fwd_kernel" in n]
-    assert len(fwd) == 28, [n for n, _ in kernels]
+    # template arguments <D, BF16, CAUSAL, NW, SPLIT, PAIR>
+    args = {n: re.search(r"fa_fwd_kernelILi(\d+)ELb(\d)ELb(\d)ELi(\d)ELb(\d)ELb(\d)E", n).groups()
+            for n, _ in fwd}
+    pair = [n for n, a in args.items() if a[5] == "1"]
+    assert len(fwd) == 32, [n for n, _ in kernels]
+    # pair mode: causal, 8 waves, unsplit, D 64/128 x fp16/bf16
+    assert len(pair) == 4 and all(args[n][2] == "1" and args[n][3] == "8" and args[n][4] == "0"
+                                  for n in pair)
     assert sum("fa_merge_kernel" in n for n, _ in kernels) == 4
     for name, f in kernels:
         assert int(f["private_segment_fixed_size"]) == 0, (name, "scratch")
@@ -66,9 +74,11 @@ def test_forward_variants_fit_two_waves_per_simd(device_asm):
         assert int(f.get("agpr_count", "0")) == 0, (name, "AGPRs")
         assert int(f["vgpr_count"]) <= 256, (name, f["vgpr_count"])
     for name, f in fwd:
-        # K/V ring: 4 tiles of 64 keys x D fp16 (+ the optimistic pass's flag).
+        # K/V ring: 4 tiles of 64 keys x D fp16, two such rings in pair mode
+        # (+ the optimistic pass's flag).
         d = 128 if "Li128E" in name else 64
-        assert int(f["group_segment_fixed_size"]) in (4 * 64 * 2 * d, 4 * 64 * 2 * d + 4), name
+        ring = (8 if name in pair else 4) * 64 * 2 * d
+        assert int(f["group_segment_fixed_size"]) in (ring, ring + 4), name
 
 
 def test_m0_only_set_for_the_staging_dma(device_asm):

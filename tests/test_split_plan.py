@@ -39,39 +39,22 @@ def tiles(qb, N, BM, causal):
 
 def check_table(pl, B, H, N, D, causal, cus=256):
     """XCD placement table: one XCD's work items (every q-tile of its heads,
-    the longest possibly in two chunks), each key tile of each (head, q-tile)
-    exactly once; the longest items run alone and the shared CUs pair long
-    with short; chunked q-tiles have their own partial slots."""
+    none split), each (head, q-tile) exactly once; the longest items run
+    alone and the shared CUs pair long with short; no workspace."""
     BM = pl.block_rows
     nq = (N + BM - 1) // BM
     hpx, cpx = B * H // 8, cus // 8
     n = pl.n_items
     assert causal and BM == 128 and B * H == 8 * pl.xcd_heads == 8 * hpx
     assert cpx < hpx * nq and n <= 2 * cpx
-    cover = {}
+    assert pl.key_halves == 1
+    assert n == hpx * nq and pl.n_merge == 0 and pl.n_slots == 0 and pl.workspace_bytes == 0
+    seen = set()
     for i in range(n):
-        key = (pl.head[i], pl.q_tile[i])
-        cover.setdefault(key, []).append((pl.tile_begin[i], pl.tile_end[i], pl.n_chunks[i],
-                                          pl.slot[i]))
-    assert sorted(cover) == [(h, q) for h in range(hpx) for q in range(nq)]
-    split_q = set()
-    for (h, q), parts in cover.items():
-        parts.sort()
-        nch = parts[0][2]
-        assert len(parts) == nch and all(x[2] == nch for x in parts) and nch in (1, 2)
-        assert parts[0][0] == 0 and parts[-1][1] == tiles(q, N, BM, causal)
-        assert all(a[1] == b[0] for a, b in zip(parts, parts[1:]))
-        if nch == 1:
-            assert parts[0][3] == -1
-        else:
-            split_q.add(q)
-            assert parts[1][3] == parts[0][3] + 1
-    # the same q-tiles split in every head, the longest ones, 2 slots each
-    k = len(split_q)
-    assert split_q == set(range(nq - k, nq))
-    assert pl.n_merge == k and pl.n_slots == 2 * k
-    assert pl.workspace_bytes == B * H * 2 * k * BM * (D * 4 + 16)
-    assert n == hpx * (nq + k)
+        assert pl.n_chunks[i] == 1 and pl.slot[i] == -1
+        assert pl.tile_begin[i] == 0 and pl.tile_end[i] == tiles(pl.q_tile[i], N, BM, causal)
+        seen.add((pl.head[i], pl.q_tile[i]))
+    assert sorted(seen) == [(h, q) for h in range(hpx) for q in range(nq)]
     lens = [pl.tile_end[i] - pl.tile_begin[i] for i in range(n)]
     m = max(n - cpx, 0)
     alone = lens[m:cpx]
@@ -83,6 +66,15 @@ def check_table(pl, B, H, N, D, causal, cus=256):
     assert firsts == sorted(firsts, reverse=True) and seconds == sorted(seconds)
     if shared:
         assert min(firsts) >= max(seconds)
+
+
+def check_pair(pl, B, H, N, causal, cus=256):
+    """Pair mode: causal, 128-row q-tiles, 0.75 to 2 of them per CU, one
+    workgroup per q-tile (no items, no workspace)."""
+    items = B * H * ((N + 127) // 128)
+    assert causal and pl.block_rows == 128 and pl.key_halves == 2
+    assert 4 * items >= 3 * cus and items < 2 * cus
+    assert pl.n_items == 0 and pl.xcd_heads == 0 and pl.workspace_bytes == 0
 
 
 def check_plan(pl, B, H, N, D, causal):
@@ -131,46 +123,64 @@ def check_plan(pl, B, H, N, D, causal):
     ("C3", 4, 32, 4096, 128, 0, A.FA_DTYPE_F16, False),
     ("C4", 2, 32, 8192, 128, 1, A.FA_DTYPE_BF16, False),
     ("C5", 1, 16, 16384, 128, 1, A.FA_DTYPE_F16, False),
-    ("C5r", 1, 16, 3000, 128, 1, A.FA_DTYPE_F16, "table"),
-    ("C5r/2", 1, 8, 3000, 128, 1, A.FA_DTYPE_F16, True),
+    ("C5r", 1, 16, 3000, 128, 1, A.FA_DTYPE_F16, "pair"),
+    ("C5r/2", 1, 8, 3000, 128, 1, A.FA_DTYPE_F16, "pair"),
+    ("C5r/4", 1, 4, 3000, 128, 1, A.FA_DTYPE_F16, True),
 ])
 def test_baseline_configs(lib, name, B, H, N, D, causal, dtype, split):
-    """The BASELINE configurations run unsplit: C2-C5 fill the machine, and
-    C5r's longest q-tile (47 key tiles) is within 1.5x of the throughput
-    bound (9584 tiles over 256 CUs x 1.1), where the partials' cost ate the
-    measured gain; C5r gets the XCD placement table instead (48 q-tiles per
-    XCD on 32 CUs).  With half its heads the same shape splits."""
+    """The BASELINE configurations run unsplit: C2-C5 fill the machine; C5r
+    (384 q-tiles of 128 rows on 256 CUs) runs in pair mode, and so does the
+    same shape with half its heads (192 = 0.75 per CU).  With a quarter of
+    its heads (96 q-tiles) the plan splits the long q-tiles instead."""
     p = contiguous(B=B, H=H, N=N, D=D, dtype=dtype, causal=causal)
     pl = plan(lib, p)
     assert pl.block_rows == (256 if (N >= 2048 and not causal) or
                              (causal and dtype == A.FA_DTYPE_F16 and N >= 8192) else 128)
-    if split == "table":
-        assert pl.xcd_heads == 2
-        check_table(pl, B, H, N, D, causal)
+    if split == "pair":
+        check_pair(pl, B, H, N, causal)
     elif not split:
         assert pl.n_items == 0 and pl.workspace_bytes == 0 and pl.n_slots == 0
+        assert pl.key_halves == 1
     else:
         assert pl.xcd_heads == 0
         check_plan(pl, B, H, N, D, causal)
 
 
-def test_c5r_table_shape(lib):
-    """C5r: 2 heads x 24 q-tiles per XCD on 32 CUs, one round.  With a
-    workspace the model cuts the 8 longest q-tiles of each head (32..47 key
-    tiles) in two, which fills all 64 slots: every CU pairs its longest
-    remaining item with its shortest (32 with 2 first, chunks of 20 last).  Without the split
-    (fa_fwd) the same table has 48 items, the 16 longest alone."""
-    pl = plan(lib, contiguous(B=1, H=16, N=3000, D=128, causal=1))
-    lens = [pl.tile_end[i] - pl.tile_begin[i] for i in range(pl.n_items)]
-    assert pl.xcd_heads == 2 and pl.n_items == 64 and pl.n_merge == 8
-    assert sorted({pl.q_tile[i] for i in range(64) if pl.n_chunks[i] == 2}) == list(range(16, 24))
-    assert (lens[0], lens[32]) == (32, 2) and (lens[31], lens[63]) == (20, 20)
-    assert max(lens) == 32
+def test_pair_mode_range(lib):
+    """Pair mode covers causal grids of 0.75 to 2 q-tiles (128 rows) per CU,
+    whatever the CU count: C5r's 384 q-tiles are in range on 256 and 512 CUs,
+    too many on 128 (plain 4-wave grid) and too few on 1024 (split-KV)."""
+    p = contiguous(B=1, H=16, N=3000, D=128, causal=1)
+    for cus in (256, 512):
+        check_pair(plan(lib, p, cus=cus), 1, 16, 3000, 1, cus)
+    small = plan(lib, p, cus=128)
+    assert small.key_halves == 1 and small.n_items == 0 and small.workspace_bytes == 0
+    big = plan(lib, p, cus=1024)
+    assert big.key_halves == 1
+    check_plan(big, 1, 16, 3000, 128, 1)
+    # non-causal and 8-wave causal problems never pair
+    for q in (contiguous(B=1, H=16, N=3000, D=128, causal=0),
+              contiguous(B=1, H=1, N=16384, D=128, causal=1)):
+        assert plan(lib, q).key_halves == 1
+
+
+@pytest.mark.parametrize("B,H,N,D,dtype", [
+    (4, 16, 1000, 64, A.FA_DTYPE_BF16),   # C2c's shape: 8 heads x 8 q-tiles per XCD
+    (2, 32, 1024, 128, A.FA_DTYPE_F16),
+])
+def test_table_at_two_qtiles_per_cu(lib, B, H, N, D, dtype):
+    """Exactly two q-tiles per CU (64 per XCD on 32 CUs): the XCD placement
+    table pairs each CU's q-tiles long with short; no CU runs alone."""
+    pl = plan(lib, contiguous(B=B, H=H, N=N, D=D, dtype=dtype, causal=1))
+    assert pl.xcd_heads == B * H // 8 and pl.n_items == 64
+    check_table(pl, B, H, N, D, 1)
+    lens = [pl.tile_end[i] - pl.tile_begin[i] for i in range(64)]
+    assert all(lens[j] + lens[32 + j] == lens[0] + lens[32] for j in range(32))
 
 
 @pytest.mark.parametrize("B,H,N,D,causal,dtype", [
-    (1, 16, 2048, 128, 1, A.FA_DTYPE_F16),
-    (1, 8, 4096, 128, 1, A.FA_DTYPE_BF16),
+    (1, 4, 2048, 128, 1, A.FA_DTYPE_F16),
+    (1, 4, 4096, 128, 1, A.FA_DTYPE_BF16),
     (1, 4, 8192, 128, 1, A.FA_DTYPE_F16),    # 8-wave causal
     (1, 1, 16384, 64, 1, A.FA_DTYPE_F16),
     (1, 2, 4096, 128, 0, A.FA_DTYPE_F16),    # few heads, non-causal
@@ -197,7 +207,9 @@ def test_plan_sweep(lib, N, causal, H):
     for D in (64, 128):
         for dtype in (A.FA_DTYPE_F16, A.FA_DTYPE_BF16):
             pl = plan(lib, contiguous(B=1, H=H, N=N, D=D, dtype=dtype, causal=causal))
-            if pl.xcd_heads:
+            if pl.key_halves == 2:
+                check_pair(pl, 1, H, N, causal)
+            elif pl.xcd_heads:
                 check_table(pl, 1, H, N, D, causal)
             elif pl.n_items:
                 check_plan(pl, 1, H, N, D, causal)
@@ -208,11 +220,11 @@ def test_plan_sweep(lib, N, causal, H):
 def test_more_cus_split_more(lib):
     """The split is a response to idle CUs: a machine with fewer CUs runs the
     same problem unsplit, a larger one splits it."""
-    p = contiguous(B=1, H=8, N=3000, D=128, causal=1)
+    p = contiguous(B=1, H=4, N=3000, D=128, causal=1)
     assert plan(lib, p, cus=8).n_items == 0
     assert plan(lib, p, cus=256).n_items > 0
     big = plan(lib, p, cus=1024)
-    check_plan(big, 1, 8, 3000, 128, 1)
+    check_plan(big, 1, 4, 3000, 128, 1)
     assert big.n_slots >= plan(lib, p, cus=256).n_slots
 
 

@@ -44,9 +44,10 @@ def _need(lib, p):
     return need.value
 
 
-# (B, H, N, D, dtype, causal, qk_sigma): the first is C5r's shape (XCD table
-# with chunks), the second a smaller bound-driven split.
-SPLIT_CASES = [(1, 16, 3000, 128, "fp16", True, 3.0), (1, 1, 4096, 64, "bf16", False, 1.0)]
+# (B, H, N, D, dtype, causal, qk_sigma): the first is C5r's shape and inputs
+# with 4 of its 16 heads (bound-driven split of the long q-tiles), the second
+# a smaller split.
+SPLIT_CASES = [(1, 4, 3000, 128, "fp16", True, 3.0), (1, 1, 4096, 64, "bf16", False, 1.0)]
 
 
 def test_scratch_matches_workspace_entry_two_calls():
@@ -95,16 +96,18 @@ def test_scratch_rejects_a_plan_beyond_its_size():
     assert torch.isnan(o).all().item() and torch.isnan(lse).all().item()
 
 
-def test_scratch_unsplit_problem_equals_fa_fwd():
+@pytest.mark.parametrize("B,H,N,causal", [(2, 8, 700, False), (1, 8, 3000, True)],
+                         ids=["plain", "pair-mode"])
+def test_scratch_unsplit_problem_equals_fa_fwd(B, H, N, causal):
     lib = A.load()
-    _note("case scratch with an unsplit problem")
-    q, k, v = _problem(2, 8, 700, 128, "fp16", False, 1.0, 4300)
+    _note(f"case scratch with an unsplit problem {B}x{H}x{N} causal={causal}")
+    q, k, v = _problem(B, H, N, 128, "fp16", causal, 1.0, 4300)
     o_ref, lse_ref = _outputs(q)
-    p_ref = A.params_from_tensors(q, k, v, o_ref, lse_ref, False)
+    p_ref = A.params_from_tensors(q, k, v, o_ref, lse_ref, causal)
     assert _need(lib, p_ref) == 0
     assert lib.fa_fwd(ctypes.byref(p_ref), None) == A.FA_OK
     o, lse = _outputs(q)
-    p = A.params_from_tensors(q, k, v, o, lse, False)
+    p = A.params_from_tensors(q, k, v, o, lse, causal)
     assert lib.fa_fwd_scratch(ctypes.byref(p), None) == A.FA_OK
     torch.cuda.synchronize()
     assert torch.equal(o, o_ref) and torch.equal(lse, lse_ref)
