@@ -87,18 +87,36 @@ __device__ __forceinline__ float dot2_acc(uint32_t w, float acc) {
 
 // Row sums of P on the matrix core.  A P^T chunk register (the B operand of
 // the 32x32x16 PV product: lane l holds 8 keys of query row l % 32, key half
-// l / 32) read as the B operand of v_mfma_f32_16x16x32_f16 has
+// l / 32) read as the B operand of v_mfma_f32_16x16x32_{f16,bf16} has
 // B[k = 8*(l/16) + j][n = l % 16]: k-groups 0 and 2 are rows 0..15, groups
 // 1 and 3 rows 16..31.  With the selector A (row 0 = ones on k-groups 0 and 2,
 // row 1 = ones on groups 1 and 3, other rows 0) the product adds the chunk's
 // 16-key sum of row n to C[0][n] and of row n + 16 to C[1][n]; lane n < 16
-// holds C[0][n] in element 0 and C[1][n] in element 1.
-__device__ __forceinline__ f16x8 row_sum_selector(int lane) {
-  const _Float16 one = ((lane & 15) == ((lane >> 4) & 1)) ? (_Float16)1.0f : (_Float16)0.0f;
-  return f16x8{one, one, one, one, one, one, one, one};
+// holds C[0][n] in element 0 and C[1][n] in element 1 (every other element
+// of the accumulator stays 0).
+template <bool BF16>
+__device__ __forceinline__ i16x8 row_sum_selector(int lane) {
+  const short one = BF16 ? (short)0x3F80 : (short)0x3C00;  // 1.0 in bf16 / fp16
+  const short v = ((lane & 15) == ((lane >> 4) & 1)) ? one : (short)0;
+  return i16x8{v, v, v, v, v, v, v, v};
 }
-__device__ __forceinline__ f32x4 row_sum_mfma(f16x8 sel, i16x8 p, f32x4 acc) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_f16(sel, __builtin_bit_cast(f16x8, p), acc, 0, 0, 0);
+template <bool BF16>
+__device__ __forceinline__ f32x4 row_sum_mfma(i16x8 sel, i16x8 p, f32x4 acc) {
+  if constexpr (BF16) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, sel),
+                                                   __builtin_bit_cast(bf16x8, p), acc, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, sel),
+                                                  __builtin_bit_cast(f16x8, p), acc, 0, 0, 0);
+  }
+}
+// Scale the row sums by a per-row factor held, like every per-row value of
+// the S^T layout, by lane l for row l % 32 (all lanes active).
+__device__ __forceinline__ f32x4 row_sum_scale(f32x4 acc, float f, int lane) {
+  const float f_hi = __shfl(f, (lane & 15) + 16);  // row n + 16's factor, for lane n
+  acc[0] *= f;
+  acc[1] *= f_hi;
+  return acc;
 }
 // The accumulated sum of lane `lane`'s query row (row lane % 32).
 __device__ __forceinline__ float row_sum_of_lane(f32x4 acc, int lane) {

@@ -182,6 +182,14 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
   // +6…10 % on narrower such grids.  The 32 extra live VGPRs fit the 8-wave
   // kernels (at most 254) and D = 64; the 4-wave D = 128 kernels would spill.
   constexpr bool kRescaleP = NW == 8 || D == 64;
+  // bf16 checked pass on 4-wave D = 128 grids: the sum of the rounded P
+  // (O's normaliser) is taken on the matrix core, 4 row_sum_mfma per tile, in
+  // place of 16 v_dot2c; the check and the LSE keep the unrounded fp32 sum.
+  // The sums are rescaled with O on a re-derivation.  Measured +0.7…1.1 % at
+  // C4, up to +4.7 % with Q, K ~ N(0, 3^2); -1 % on split grids (few heads),
+  // which keep v_dot2c.  The 8-wave and D = 64 kernels have no VGPRs left
+  // for it next to kRescaleP.
+  constexpr bool kMfmaNorm = kUnroundedSum && !kRescaleP && !SPLIT;
   static_assert(ITERS >= 1 && T::BYTES % (1024 * NWD) == 0, "tile must split evenly over waves");
 
   // LDS ring: K buffers 0/1 then V buffers 0/1 (pair mode: K 0/1 of each
@@ -369,8 +377,8 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
   float neg_mc = INFINITY;  // -m_run * c; +inf while m_run = -inf (trips the first check)
   float l_run = 0.0f;       // this lane's partial sum of P (unrounded p when kUnroundedSum)
   float lr_run = 0.0f;      // kUnroundedSum: this lane's partial sum of the rounded P
-  f32x4 l_mfma = {0.0f, 0.0f, 0.0f, 0.0f};  // row sums on the matrix core (kMfmaSums)
-  const f16x8 sum_sel = row_sum_selector(lane);
+  f32x4 l_mfma = {0.0f, 0.0f, 0.0f, 0.0f};  // row sums on the matrix core (kMfmaSums, kMfmaNorm)
+  const i16x8 sum_sel = row_sum_selector<BF16>(lane);
 
   // Per-lane LDS byte offsets inside a tile (loop invariant).
   // K: A operand of key block 0, k-step kk (block 1: + 32 rows).
@@ -490,7 +498,7 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
             // the rounded P for the normalisation.
             t0 += p0;
             t1 += p1;
-            tr = dot2_acc<BF16>(w[j], tr);
+            if constexpr (!kMfmaNorm) tr = dot2_acc<BF16>(w[j], tr);
           }
         }
         pf[ch] = __builtin_bit_cast(i16x8, w);
@@ -564,7 +572,8 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
       const float alpha = fast_exp2(grow ? (m_run - m_new) * c : 0.0f);
       m_run = m_new;
       l_run *= alpha;
-      if constexpr (kUnroundedSum) lr_run *= alpha;
+      if constexpr (kUnroundedSum && !kMfmaNorm) lr_run *= alpha;
+      if constexpr (kMfmaNorm && !OPT) l_mfma = row_sum_scale(l_mfma, alpha, lane);
 #pragma unroll
       for (int db = 0; db < DBLK; ++db)
 #pragma unroll
@@ -595,7 +604,7 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
     }
     if constexpr (!OPT) {
       l_run += t0 + t1;
-      if constexpr (kUnroundedSum) lr_run += tr;
+      if constexpr (kUnroundedSum && !kMfmaNorm) lr_run += tr;
     }
 
     // ---- O^T += V^T P^T ----
@@ -608,7 +617,8 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
       constexpr int j = decltype(j_c)::value;
       constexpr int db = j % DBLK, ch = j / DBLK;
       o_acc[db] = Ops::mfma(va[j % VD], pf[ch], o_acc[db]);
-      if constexpr (OPT && db == DBLK - 1) l_mfma = row_sum_mfma(sum_sel, pf[ch], l_mfma);
+      if constexpr ((OPT || kMfmaNorm) && db == DBLK - 1)
+        l_mfma = row_sum_mfma<BF16>(sum_sel, pf[ch], l_mfma);
       if constexpr (j + VD < NPV) {
         constexpr int db2 = (j + VD) % DBLK, ch2 = (j + VD) / DBLK;
         constexpr int off = (2 + BUF) * T::BYTES + ch2 * 16 * T::ROWB;
@@ -670,7 +680,7 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
   } else {
     run_tiles(std::false_type{});
     l_tot = pair_sum(l_run);
-    lr_tot = kUnroundedSum ? pair_sum(lr_run) : l_tot;
+    lr_tot = kMfmaNorm ? row_sum_of_lane(l_mfma, lane) : kUnroundedSum ? pair_sum(lr_run) : l_tot;
   }
 
   if constexpr (PAIR) {

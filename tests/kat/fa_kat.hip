@@ -206,31 +206,42 @@ extern "C" int kat_xcd_remap(int total, int* out) {
   return rc;
 }
 
-// row_sum_mfma / row_sum_of_lane over two P chunks: lane l holds 8 fp16
-// values (bits in p_bits[(c*64 + l)*8 ..]) of chunk c; out[l] receives the
-// sum over both chunks of row l % 32 (lanes l%32 and l%32 + 32).
-__global__ void kat_row_sum_kernel(const i16x8* p, float* out) {
+// row_sum_mfma / row_sum_of_lane over two P chunks: lane l holds 8 fp16 or
+// bf16 values (bits in p_bits[(c*64 + l)*8 ..]) of chunk c; out[l] receives
+// the sum over both chunks of row l % 32 (lanes l%32 and l%32 + 32), the
+// first chunk's sums scaled by row_sum_scale with the factor of row r held
+// in f[r] and f[r + 32] (as the kernel holds per-row values).
+template <bool BF16>
+__global__ void kat_row_sum_kernel(const i16x8* p, const float* f, float* out) {
   const int l = threadIdx.x;
   f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-  const f16x8 sel = row_sum_selector(l);
-  acc = row_sum_mfma(sel, p[l], acc);
-  acc = row_sum_mfma(sel, p[64 + l], acc);
+  const i16x8 sel = row_sum_selector<BF16>(l);
+  acc = row_sum_mfma<BF16>(sel, p[l], acc);
+  acc = row_sum_scale(acc, f[l], l);
+  acc = row_sum_mfma<BF16>(sel, p[64 + l], acc);
   out[l] = row_sum_of_lane(acc, l);
 }
 
-extern "C" int kat_row_sum(const uint16_t* p_bits, float* out) {
-  void *dp = 0, *dout = 0;
+extern "C" int kat_row_sum(const uint16_t* p_bits, const float* f, int bf16, float* out) {
+  void *dp = 0, *df = 0, *dout = 0;
   int rc = check(hipMalloc(&dp, 2 * 64 * 8 * 2));
+  if (!rc) rc = check(hipMalloc(&df, 64 * 4));
   if (!rc) rc = check(hipMalloc(&dout, 64 * 4));
   if (!rc) rc = check(hipMemcpy(dp, p_bits, 2 * 64 * 8 * 2, hipMemcpyHostToDevice));
+  if (!rc) rc = check(hipMemcpy(df, f, 64 * 4, hipMemcpyHostToDevice));
   if (!rc) {
-    hipLaunchKernelGGL(kat_row_sum_kernel, dim3(1), dim3(64), 0, 0, (const i16x8*)dp,
-                       (float*)dout);
+    if (bf16)
+      hipLaunchKernelGGL(kat_row_sum_kernel<true>, dim3(1), dim3(64), 0, 0, (const i16x8*)dp,
+                         (const float*)df, (float*)dout);
+    else
+      hipLaunchKernelGGL(kat_row_sum_kernel<false>, dim3(1), dim3(64), 0, 0, (const i16x8*)dp,
+                         (const float*)df, (float*)dout);
     rc = check(hipGetLastError());
   }
   if (!rc) rc = check(hipDeviceSynchronize());
   if (!rc) rc = check(hipMemcpy(out, dout, 64 * 4, hipMemcpyDeviceToHost));
   if (dp) (void)hipFree(dp);
+  if (df) (void)hipFree(df);
   if (dout) (void)hipFree(dout);
   return rc;
 }

@@ -27,7 +27,7 @@ def kat():
     L.kat_pair.argtypes = [fp, fp, fp]
     L.kat_dma.argtypes = [ctypes.POINTER(ctypes.c_int32)]
     L.kat_xcd_remap.argtypes = [ctypes.c_int, ctypes.POINTER(ctypes.c_int32)]
-    L.kat_row_sum.argtypes = [u16p, fp]
+    L.kat_row_sum.argtypes = [u16p, fp, ctypes.c_int, fp]
     return L
 
 
@@ -190,19 +190,29 @@ def test_xcd_remap_is_contiguous_per_xcd(kat, total):
         assert np.all(np.diff(out[np.arange(total) % 8 == x]) == 1)
 
 
-def test_row_sum_mfma_lane_map(kat):
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+def test_row_sum_mfma_lane_map(kat, dtype):
     """row_sum_mfma: the 16x16x32 MFMA with the selector operand sums each
     query row's keys of a P^T chunk (lane l: row l % 32, key half l / 32),
-    and row_sum_of_lane hands every lane its row's total."""
-    print("case row_sum_mfma", flush=True)
+    row_sum_scale multiplies each row's running sum by that row's factor,
+    and row_sum_of_lane hands every lane its row's total.  Values k/64 with
+    k < 256 are exact in both types, so the sums are exact."""
+    print(f"case row_sum_mfma {dtype}", flush=True)
     rng = np.random.default_rng(9)
-    vals = rng.uniform(0.0, 4.0, size=(2, 64, 8)).astype(np.float16)
-    bits = np.ascontiguousarray(vals.view(np.uint16))
+    vals = rng.integers(0, 256, size=(2, 64, 8)).astype(np.float32) / 64.0
+    if dtype == "fp16":
+        bits = np.ascontiguousarray(vals.astype(np.float16).view(np.uint16))
+    else:
+        bits = np.ascontiguousarray((vals.view(np.uint32) >> 16).astype(np.uint16))
+    row_f = rng.integers(1, 9, size=32).astype(np.float32) / 8.0   # exact factors
+    f = np.concatenate([row_f, row_f]).astype(np.float32)
     out = np.zeros(64, np.float32)
     u16p = ctypes.POINTER(ctypes.c_uint16)
     fp = ctypes.POINTER(ctypes.c_float)
-    assert kat.kat_row_sum(bits.ctypes.data_as(u16p), out.ctypes.data_as(fp)) == 0
-    per_lane = vals.astype(np.float64).sum(axis=(0, 2))      # both chunks, 8 keys
-    rows = per_lane[:32] + per_lane[32:]                      # the two key halves
+    assert kat.kat_row_sum(bits.ctypes.data_as(u16p), f.ctypes.data_as(fp),
+                           1 if dtype == "bf16" else 0, out.ctypes.data_as(fp)) == 0
+    lane_sums = vals.astype(np.float64).sum(axis=2)           # [chunk, lane]
+    row_sums = lane_sums[:, :32] + lane_sums[:, 32:]          # [chunk, row]: both key halves
+    rows = row_sums[0] * row_f + row_sums[1]
     expect = np.concatenate([rows, rows])
-    assert np.allclose(out, expect, rtol=1e-6, atol=1e-4), (out[:8], expect[:8])
+    assert np.array_equal(out, expect.astype(np.float32)), (out[:8], expect[:8])
