@@ -101,6 +101,7 @@ void to_kernel_args(const fa_fwd_params* p, fa::KernelArgs* a) {
   a->split.n_merge = 0;
   a->split.xcd_heads = 0;
   a->split.pair = 0;
+  a->split.head_group = 0;
 }
 
 // Compute units of the calling thread's current device (queried once per
@@ -271,6 +272,7 @@ fa_status fa_fwd_plan(const fa_fwd_params* p, int32_t compute_units, fa_fwd_plan
   out->n_merge = a.split.n_merge;
   out->xcd_heads = a.split.xcd_heads;
   out->key_halves = a.split.pair ? 2 : 1;
+  out->head_group = a.split.head_group;
   for (int i = 0; i < a.split.n_items; ++i) {
     const uint32_t info = a.split.item[i];
     const int qb = (int)(info & 0xffffu), c = (int)((info >> 16) & 0xffu), nch = (int)(info >> 24);

@@ -18,12 +18,10 @@ namespace fa {
 // a second kernel.  Used when the grid would leave most of the machine idle
 // behind a few long q-tiles (short causal problems, few heads).
 //
-// XCD placement table (xcd_heads > 0): a causal grid of one round of two
-// workgroups per CU, where the hardware puts the k-th and (k + CUs per
-// XCD)-th workgroups of an XCD on the same CU.  The table orders each XCD's
-// work items so the longest run alone and the others share a CU long with
-// short; with a workspace it may also cut the longest q-tiles in two
-// chunks (merged as in split-KV).
+// XCD placement table (xcd_heads > 0): a causal grid of exactly two q-tiles
+// per CU, where the hardware puts the k-th and (k + CUs per XCD)-th
+// workgroups of an XCD on the same CU.  The table orders each XCD's q-tiles
+// so the longest run alone and the others share a CU long with short.
 constexpr int kMaxSplitItems = 128;
 
 struct SplitPlan {
@@ -32,6 +30,10 @@ struct SplitPlan {
   int32_t n_merge;   // q-tiles with more than one chunk (merged by the second kernel)
   int32_t xcd_heads; // > 0: XCD placement table over this many heads per XCD
   int32_t pair;      // 1: pair mode (8 waves per 128-row causal q-tile, no items)
+  // Causal grids in plain order with B*H a multiple of 8 (no items, no
+  // table): each XCD runs its heads in groups of head_group, the q-tiles of
+  // a group's heads interleaved longest first; 0 otherwise.
+  int32_t head_group;
   // Item i: q-tile (bits 0..15), chunk (16..23), chunk count (24..31).
   uint32_t item[kMaxSplitItems];
   // Item i's first partial slot of its q-tile (items of one q-tile use

@@ -242,16 +242,13 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
   } else {
     qb = CAUSAL ? args.n_qblocks - 1 - item : item;  // longest q-tiles first
     if (CAUSAL && ((args.batch * args.heads) & 7) == 0) {
-      // Whole heads per XCD, taken in groups of 4 (or all of them when their
-      // count is not a multiple of 4): longest first across a group's heads
-      // (their q-tiles interleaved), group after group.  Interleaving keeps
-      // the last head's long q-tiles from starting late (+1.5 % at B2 H32
-      // N8192 and B1 H16 N16384, +2.7 % at B1 H16 N8192 over head after
-      // head); groups of 4 instead of all 8 heads of B2 H32 N8192 shrink the
-      // XCD's K/V working set from 32 to 16 MiB (+2.3..3 % there).  Same
-      // blocks per XCD as xcd_remap.
+      // Whole heads per XCD, taken in groups of args.split.head_group (the
+      // plan's choice; all of them if it does not divide their count):
+      // longest first across a group's heads (their q-tiles interleaved),
+      // group after group.  Same blocks per XCD as xcd_remap.
       const int hpx = (args.batch * args.heads) >> 3;
-      const int grp_heads = (hpx & 3) == 0 ? 4 : hpx;
+      const int hg = args.split.head_group;
+      const int grp_heads = hg > 0 && hpx % hg == 0 ? hg : hpx;
       const int per_grp = grp_heads * args.n_qblocks;
       const int i = (int)(blockIdx.x >> 3);
       const int grp = i / per_grp, w = i - grp * per_grp;

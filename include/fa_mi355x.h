@@ -131,6 +131,10 @@ typedef struct {
   int32_t xcd_heads;        /* > 0: XCD placement table (no split) over this many heads per XCD */
   int32_t key_halves;       /* 2: pair mode (8 waves per q-tile, each half on alternate key
                                tiles, one workgroup per q-tile, no items); 1 otherwise */
+  int32_t head_group;       /* > 0: causal grid without items, B*H a multiple of 8: each XCD
+                               runs its heads in groups of this many, the q-tiles of a group
+                               interleaved longest first; 0 otherwise */
+  int32_t reserved;         /* 0 */
   uint64_t workspace_bytes; /* bytes fa_fwd_ws needs (0 when unsplit) */
   /* Split-KV (xcd_heads == 0): work item i (dispatch order, longest first)
    * of every (batch, head) is q-tile q_tile[i], key tiles (64 keys each)

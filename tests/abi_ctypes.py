@@ -81,6 +81,8 @@ class FaFwdPlan(ctypes.Structure):
         ("n_merge", ctypes.c_int32),
         ("xcd_heads", ctypes.c_int32),
         ("key_halves", ctypes.c_int32),
+        ("head_group", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
         ("workspace_bytes", ctypes.c_uint64),
         ("q_tile", ctypes.c_int32 * FA_PLAN_MAX_ITEMS),
         ("tile_begin", ctypes.c_int32 * FA_PLAN_MAX_ITEMS),

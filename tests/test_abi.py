@@ -114,6 +114,7 @@ int main(void) {
   F(fa_device_info_t, arch_major); F(fa_device_info_t, arch_minor); F(fa_device_info_t, reserved);
   F(fa_fwd_plan_t, block_rows); F(fa_fwd_plan_t, n_items); F(fa_fwd_plan_t, n_slots);
   F(fa_fwd_plan_t, n_merge); F(fa_fwd_plan_t, xcd_heads); F(fa_fwd_plan_t, key_halves);
+  F(fa_fwd_plan_t, head_group); F(fa_fwd_plan_t, reserved);
   F(fa_fwd_plan_t, workspace_bytes);
   F(fa_fwd_plan_t, q_tile); F(fa_fwd_plan_t, tile_begin); F(fa_fwd_plan_t, tile_end);
   F(fa_fwd_plan_t, n_chunks); F(fa_fwd_plan_t, slot); F(fa_fwd_plan_t, head);

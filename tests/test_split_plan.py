@@ -146,6 +146,33 @@ def test_baseline_configs(lib, name, B, H, N, D, causal, dtype, split):
         check_plan(pl, B, H, N, D, causal)
 
 
+@pytest.mark.parametrize("B,H,N,dtype,causal,cus,group", [
+    (2, 32, 8192, A.FA_DTYPE_BF16, 1, 256, 2),   # C4: 8 heads per XCD, 64 q-tiles each
+    (2, 32, 8192, A.FA_DTYPE_BF16, 1, 304, 4),   # 38 CUs per XCD: a pair is under 2 rounds
+    (4, 32, 4096, A.FA_DTYPE_F16, 1, 256, 4),    # 32 q-tiles per head: 4 heads for 2 rounds
+    (8, 32, 1024, A.FA_DTYPE_F16, 1, 256, 4),
+    (1, 16, 16384, A.FA_DTYPE_F16, 1, 256, 2),   # C5: 2 heads per XCD, 8-wave
+    (2, 8, 8192, A.FA_DTYPE_BF16, 1, 256, 2),
+    (1, 24, 8192, A.FA_DTYPE_F16, 1, 256, 3),    # 3 heads per XCD: one group
+    (1, 16, 3000, A.FA_DTYPE_F16, 1, 256, 2),    # C5r, pair mode
+    (1, 12, 4096, A.FA_DTYPE_F16, 1, 256, 0),    # B*H not a multiple of 8
+    (4, 32, 4096, A.FA_DTYPE_F16, 0, 256, 0),    # non-causal
+    (1, 16, 4096, A.FA_DTYPE_F16, 1, 256, 0),    # XCD placement table
+    (1, 4, 3000, A.FA_DTYPE_F16, 1, 256, 0),     # split-KV
+])
+def test_causal_head_group(lib, B, H, N, dtype, causal, cus, group):
+    """Causal grids in plain order (no items) with B*H a multiple of 8 run
+    each XCD's heads in groups: 4 when the XCD's head count is a multiple of
+    4, else all of them, and 2 when a group of 2 heads still fills the XCD's
+    workgroup slots (two per CU for 128-row q-tiles, one otherwise) twice.
+    The group always divides the XCD's head count."""
+    p = contiguous(B=B, H=H, N=N, D=128, dtype=dtype, causal=causal)
+    pl = plan(lib, p, cus)
+    assert pl.head_group == group and pl.reserved == 0
+    if group:
+        assert pl.n_items == 0 and (B * H // 8) % group == 0
+
+
 def test_pair_mode_range(lib):
     """Pair mode covers causal grids of 0.75 to 2 q-tiles (128 rows) per CU,
     whatever the CU count: C5r's 384 q-tiles are in range on 256 and 512 CUs,
