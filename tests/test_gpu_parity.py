@@ -30,8 +30,9 @@ def _note(msg):
     print(msg, flush=True)
 
 
-def _fwd(fa, q, k, v, causal, scale=None):
-    o, lse = fa.forward(q, k, v, causal=causal, softmax_scale=scale, return_lse=True)
+def _fwd(fa, q, k, v, causal, scale=None, split_kv=True):
+    o, lse = fa.forward(q, k, v, causal=causal, softmax_scale=scale, return_lse=True,
+                        split_kv=split_kv)
     torch.cuda.synchronize()
     return o, lse
 
@@ -106,7 +107,9 @@ def _scale_keys(k, pattern):
     ramp  - key j x (1 + 6j/N): the max rises on every tile;
     half  - keys j = 4..7 mod 8 of tile 2 x8: only one lane half of each row
             (keys 8a + 4g + b, g = lane half) sees the jump;
-    drop  - tile 0 x8: the first tile holds the max, later P are tiny."""
+    drop  - tile 0 x8: the first tile holds the max, later P are tiny;
+    huge  - tile 3 x60: the scores jump by more than 126 log2 units, past
+            what a P kept in fp32 with the old offset can hold."""
     k = k.float()
     N = k.shape[2]
     f = torch.ones(N)
@@ -119,6 +122,8 @@ def _scale_keys(k, pattern):
         f[(j >= 128) & (j < 192) & (j % 8 >= 4)] = 8.0
     elif pattern == "drop":
         f[:64] = 8.0
+    elif pattern == "huge":
+        f[192:256] = 60.0
     return k * f[None, None, :, None]
 
 
@@ -140,18 +145,57 @@ def test_score_jumps_vs_oracle(fa, oracle, pattern, causal, dtype):
     _check_against_oracle(oracle, q, k, v, o, lse, causal, scale, dtype, contract=False)
 
 
-@pytest.mark.parametrize("pattern", ["jump", "ramp", "drop"])
-def test_score_jumps_wide_workgroup_vs_oracle(fa, oracle, pattern):
+@pytest.mark.parametrize("pattern", ["jump", "ramp", "drop", "huge"])
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+def test_score_jumps_wide_workgroup_vs_oracle(fa, oracle, pattern, dtype):
     """The same score jumps on the 8-wave workgroup (non-causal, N >= 2048):
-    the optimistic pass of fp16 D=128 overflows on "jump" and "ramp", and the
-    workgroup is recomputed with per-tile checks."""
-    _note(f"case jumps wide pattern={pattern}")
+    the optimistic pass of fp16 D=128 overflows on "jump", "ramp" and "huge",
+    and the workgroup is recomputed with per-tile checks; bf16 runs only the
+    checked pass.  Its re-derivations rescale the kept fp32 P, except for
+    "huge", where that P is inf and is computed again."""
+    _note(f"case jumps wide pattern={pattern} {dtype}")
     N, D = 2304, 128
-    q, k, v = make_qkv(1, 2, N, D, "fp16", seed=case_seed(778), device="cpu")
-    k = _scale_keys(k, pattern).to(torch.float16)
+    q, k, v = make_qkv(1, 2, N, D, dtype, seed=case_seed(778), device="cpu")
+    tdt = torch.float16 if dtype == "fp16" else torch.bfloat16
+    k = _scale_keys(k, pattern).to(tdt)
     scale = 1.0 / math.sqrt(D)
     o, lse = _fwd(fa, q.to(DEV), k.to(DEV), v.to(DEV), False)
-    _check_against_oracle(oracle, q, k, v, o, lse, False, scale, "fp16", contract=False)
+    _check_against_oracle(oracle, q, k, v, o, lse, False, scale, dtype, contract=False)
+
+
+@pytest.mark.parametrize("pattern", ["jump", "half", "ramp", "huge"])
+@pytest.mark.parametrize("causal", [False, True], ids=["noncausal", "causal"])
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+@pytest.mark.parametrize("D", [64, 128])
+def test_score_jumps_plain_grid_vs_oracle(fa, oracle, pattern, causal, dtype, D):
+    """Score jumps on the unsplit grid (split_kv=False; N = 640 would
+    otherwise be split).  At D = 64 the checked pass keeps P in fp32 and
+    rescales it on a re-derivation ("huge": computed again instead); bf16 at
+    D = 128 sums the rounded P on the matrix core and rescales those sums
+    with O."""
+    _note(f"case jumps plain pattern={pattern} {dtype} D={D} causal={causal}")
+    N = 640
+    q, k, v = make_qkv(1, 2, N, D, dtype, seed=case_seed(779 + D), device="cpu")
+    tdt = torch.float16 if dtype == "fp16" else torch.bfloat16
+    k = _scale_keys(k, pattern).to(tdt)
+    scale = 1.0 / math.sqrt(D)
+    o, lse = _fwd(fa, q.to(DEV), k.to(DEV), v.to(DEV), causal, split_kv=False)
+    _check_against_oracle(oracle, q, k, v, o, lse, causal, scale, dtype, contract=False)
+
+
+@pytest.mark.parametrize("pattern", ["jump", "huge"])
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+def test_score_jumps_pair_mode_vs_oracle(fa, oracle, pattern, dtype):
+    """Score jumps in pair mode (B1 H8 N3000 causal: 192 q-tiles of 128 rows
+    on 256 CUs), whose 8-wave checked pass rescales the kept fp32 P."""
+    _note(f"case jumps pair pattern={pattern} {dtype}")
+    N, D = 3000, 128
+    q, k, v = make_qkv(1, 8, N, D, dtype, seed=case_seed(780), device="cpu")
+    tdt = torch.float16 if dtype == "fp16" else torch.bfloat16
+    k = _scale_keys(k, pattern).to(tdt)
+    scale = 1.0 / math.sqrt(D)
+    o, lse = _fwd(fa, q.to(DEV), k.to(DEV), v.to(DEV), True)
+    _check_against_oracle(oracle, q, k, v, o, lse, True, scale, dtype, contract=False)
 
 
 @pytest.mark.parametrize("case", range(24))
