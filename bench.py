@@ -7,7 +7,9 @@ A step is one forward over one batch of synthetic input already resident in
 HBM: flash_attention_runtime.forward(q, k, v, o) on the headline workload C3
 (B=4, H=32, N=4096, D=128, fp16, non-causal; Q, K, V ~ N(0, 1) from seed
 1234 + 100003*2, the reference's convention in
-benchmark/python/input_data.py:11-30).  W untimed warmup steps, then K steps
+benchmark/python/input_data.py:11-30).  W untimed warmup steps (default 1000,
+about a second of C3: the power-limited chip's clock is still rising after
+the first hundred launches on a fresh GPU), then K steps
 timed by two HIP events on the stream the kernel is launched on, bracketed by
 device synchronisation.  FLOPs per step = 4*B*H*N^2*D (halved for causal).
 
@@ -111,7 +113,7 @@ def gemm_ceiling(torch, steps, warmup):
                     a = torch.ones((n, n), device="cuda", dtype=dt)
                     b = torch.ones((n, n), device="cuda", dtype=dt)
                 c = torch.empty((n, n), device="cuda", dtype=dt)
-                for _ in range(max(warmup, 3)):
+                for _ in range(min(max(warmup, 3), 20)):  # GEMMs of ms each
                     torch.matmul(a, b, out=c)
                 reps = max(5, min(steps, 50))
                 start = torch.cuda.Event(enable_timing=True)
@@ -243,7 +245,7 @@ def main():
     ap = argparse.ArgumentParser(description="MI355X FlashAttention-2 forward benchmark")
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=1000)
     ap.add_argument("--workload", default="C3", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--all", action="store_true", help="also time every config (stderr table)")
