@@ -2,6 +2,7 @@
 
 Outputs (next to the Python package, so they travel with the repository):
   flash_attention_runtime/libfa_mi355x.so   HIP kernels + C ABI (hipcc, gfx950)
+  flash_attention_runtime/libfa_mi355x_poison.so   the same with LDS poisoning (tests only)
   flash_attention_runtime/_C<EXT_SUFFIX>     torch/pybind binding over the C ABI
   flash_attention_runtime/fa_profile         C++ benchmark CLI over the C ABI
   flash_attention_runtime/fa_device_query    device description CLI over the C ABI
@@ -62,31 +63,39 @@ def _hipcc() -> str:
     raise RuntimeError("hipcc not found")
 
 
-def build_hip_library(jobs: int) -> str:
+def build_hip_library(jobs: int) -> list[str]:
     """Compiles csrc/fa_fwd_kernel.hip (kernels and launch), fa_plan.cpp
     (host work planning) and fa_api.cpp (the C ABI) with hipcc and links the
-    shared library libfa_mi355x.so."""
+    shared library libfa_mi355x.so.  The kernel source is compiled a second
+    time with -DFA_LDS_POISON into the debug library
+    libfa_mi355x_poison.so (same ABI; staged LDS is filled with NaN before
+    every staging write), which only the tests load."""
     os.makedirs(BUILD_DIR, exist_ok=True)
     hipcc = _hipcc()
-    sources = [
-        os.path.join(CSRC, "fa_fwd_kernel.hip"),
-        os.path.join(CSRC, "fa_plan.cpp"),
-        os.path.join(CSRC, "fa_api.cpp"),
-    ]
-    objs = []
+    kernel = os.path.join(CSRC, "fa_fwd_kernel.hip")
+    host = [os.path.join(CSRC, "fa_plan.cpp"), os.path.join(CSRC, "fa_api.cpp")]
+
+    def obj_of(src: str, tag: str = "") -> str:
+        return os.path.join(BUILD_DIR, os.path.basename(src) + tag + ".o")
+
     cmds = []
-    for src in sources:
-        obj = os.path.join(BUILD_DIR, os.path.basename(src) + ".o")
-        objs.append(obj)
+    for src in [kernel, *host]:
         lang = ["-x", "hip"] if src.endswith(".hip") else []
-        cmds.append([hipcc, *HIP_FLAGS, "-I", INCLUDE, "-I", CSRC, *lang, "-c", src, "-o", obj])
+        cmds.append([hipcc, *HIP_FLAGS, "-I", INCLUDE, "-I", CSRC, *lang, "-c", src,
+                     "-o", obj_of(src)])
+    cmds.append([hipcc, *HIP_FLAGS, "-DFA_LDS_POISON", "-I", INCLUDE, "-I", CSRC, "-x", "hip",
+                 "-c", kernel, "-o", obj_of(kernel, ".poison")])
     with ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
         list(ex.map(_run, cmds))
-    lib = os.path.join(OUT_DIR, "libfa_mi355x.so")
-    tmp = lib + ".tmp"
-    _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp])
-    os.replace(tmp, lib)
-    return lib
+    libs = []
+    for name, kobj in (("libfa_mi355x.so", obj_of(kernel)),
+                       ("libfa_mi355x_poison.so", obj_of(kernel, ".poison"))):
+        lib = os.path.join(OUT_DIR, name)
+        _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", kobj,
+              *[obj_of(h) for h in host], "-o", lib + ".tmp"])
+        os.replace(lib + ".tmp", lib)
+        libs.append(lib)
+    return libs
 
 
 def build_torch_binding() -> str:
@@ -150,12 +159,12 @@ def build_mfma_probe() -> str:
 
 
 def build(jobs: int = 8) -> list[str]:
-    lib = build_hip_library(jobs)
+    libs = build_hip_library(jobs)
     ext = build_torch_binding()
     cli = build_profile_cli()
     query = build_device_query()
     probe = build_mfma_probe()
-    return [lib, ext, cli, query, probe]
+    return [*libs, ext, cli, query, probe]
 
 
 def main() -> None:

@@ -103,6 +103,20 @@ using lds::dma_slot;
 // far from overflow in the fp32 O and l accumulators.  When it is re-derived,
 // m moves to the row max for rows that exceed it by more than
 // kRescaleThreshold (log2 units).
+// LDS-poison debug build (compiled with -DFA_LDS_POISON, shipped as
+// libfa_mi355x_poison.so, never the product library): every wave fills the
+// LDS bytes it is about to stage (K/V ring slots, staged Q, the output
+// rows, the pair-mode combine area) with all-ones words, NaN in fp16, bf16
+// and fp32, and waits for the fill before the staging write.  A read that
+// raced ahead of its wait or barrier then sees NaN instead of the previous
+// tile's plausible values; with correct synchronisation the output is bit
+// for bit that of the product build.
+#ifdef FA_LDS_POISON
+constexpr bool kLdsPoison = true;
+#else
+constexpr bool kLdsPoison = false;
+#endif
+
 constexpr float kSumLimit = 32768.0f;
 constexpr float kRescaleThreshold = 8.0f;
 
@@ -296,6 +310,11 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
   }
   const uint32_t smem_base = __builtin_amdgcn_readfirstlane(lds_addr(smem));
   const uint32_t wave_dma_base = smem_base + rw * ITERS * 1024;
+  // kLdsPoison: fill the KiB at LDS byte offset `off` (from smem), 16 bytes
+  // per lane, as one wave's staging instruction covers it.
+  auto poison_kib = [&](uint32_t off) FA_INLINE {
+    *reinterpret_cast<u32x4*>(smem + off + lane * 16) = u32x4{~0u, ~0u, ~0u, ~0u};
+  };
 
   // Stage K and V rows [t*BN, t*BN + BN) into LDS buffer `buf`.
   auto issue_tile = [&](int t, int buf) FA_INLINE {
@@ -304,6 +323,14 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
     const char* vbase = vh + row0 * vsb;
     const uint32_t kdst = wave_dma_base + (kslot + buf) * T::BYTES;
     const uint32_t vdst = wave_dma_base + (vslot + buf) * T::BYTES;
+    if constexpr (kLdsPoison) {
+#pragma unroll
+      for (int it = 0; it < ITERS; ++it) {
+        poison_kib(kdst - smem_base + it * 1024);
+        poison_kib(vdst - smem_base + it * 1024);
+      }
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the fill lands before the DMA
+    }
     if (row0 + BN <= N) {
 #pragma unroll
       for (int it = 0; it < ITERS; ++it) dma_16b(k_src[it], kbase, kdst + it * 1024);
@@ -344,6 +371,11 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
   if constexpr (kStageQ) {
     const int qr0 = min(wrow0, N - 1);
     const char* qbase = qh + qr0 * qsb;
+    if constexpr (kLdsPoison) {
+#pragma unroll
+      for (int it = 0; it < KSTEPS; ++it) poison_kib(q_lds + it * 1024);
+      __builtin_amdgcn_s_waitcnt(0xc07f);
+    }
 #pragma unroll
     for (int it = 0; it < KSTEPS; ++it) {  // 32 rows x QRB bytes = KSTEPS x 1 KiB
       // DMA lane destinations are fixed (16 bytes per lane): fetch the chunk
@@ -685,9 +717,17 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
     // the sums to their row partners through LDS, above the rows the
     // epilogue stages; each half's terms are rescaled to the larger offset.
     constexpr int XO = DBLK * 16 * 64;  // floats of O per wave
+    static_assert((XO + 4 * 64) * 4 % 1024 == 0 &&
+                      256 * D + 4 * (XO + 4 * 64) * 4 <= 8 * T::BYTES,
+                  "the combine area (whole KiB per wave) lies inside the ring");
     float* xo = reinterpret_cast<float*>(smem + 256 * D) + rw * (XO + 4 * 64);
     float* xm = xo + XO;
     if (half == 1) {
+      if constexpr (kLdsPoison) {
+        const uint32_t off = (uint32_t)(reinterpret_cast<char*>(xo) - smem);
+        for (int kib = 0; kib < (XO + 4 * 64) * 4 / 1024; ++kib) poison_kib(off + kib * 1024);
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+      }
 #pragma unroll
       for (int db = 0; db < DBLK; ++db)
 #pragma unroll
@@ -724,6 +764,10 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
                         FA_INLINE {
     const int nc = rowb >> 4;
     char* ot = smem + wave * 32 * rowb;
+    if constexpr (kLdsPoison) {
+      for (int kib = 0; kib < rowb / 32; ++kib) poison_kib(wave * 32 * rowb + kib * 1024);
+      __builtin_amdgcn_s_waitcnt(0xc07f);
+    }
     put([&](int r, int c, auto w) FA_INLINE {
       *reinterpret_cast<decltype(w)*>(ot + lds::row_tile_offset(r, c, rowb)) = w;
     });

@@ -78,6 +78,20 @@ def test_exported_symbols_are_c_linkage():
         assert n in exported, f"{n} is not an unmangled text symbol"
 
 
+def test_poison_build_exports_the_same_abi():
+    """The LDS-poison debug library (tests only) is built beside the product
+    one, loads on a host without a GPU, and exports every declared function
+    unmangled, so any test can run against it in place of the product."""
+    if not os.path.exists(A.POISON_LIB_PATH):
+        pytest.skip("run build() first: no LDS-poison library")
+    L = A.load(A.POISON_LIB_PATH)
+    out = subprocess.run(["nm", "-D", "--defined-only", A.POISON_LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
+    for n in A.declared_functions():
+        assert hasattr(L, n) and n in exported, n
+
+
 def test_status_enum_matches_header():
     text = open(A.HEADER).read()
     import re
