@@ -228,6 +228,54 @@ def test_random_problems_vs_oracle(fa, oracle, case):
     _check_against_oracle(oracle, q, k, v, o, lse, causal, scale, dtype, contract=False)
 
 
+@pytest.mark.parametrize("case", range(32))
+def test_random_grids_vs_oracle(fa, oracle, case):
+    """Seeded random problems of the sizes where the work plans differ: pair
+    mode, split-KV, the XCD placement table, 8-wave workgroups, head groups
+    (H and N drawn per case, B = 1 or 2), Q, K ~ N(0, s^2) with s in
+    {1, 2, 3} (mid-row re-derivations), with and without split_kv.  Sampled
+    rows (edges, tile boundaries and random ones) of the first, middle and
+    last head against the fp64 oracle and the emulator, at the same bars as
+    the other non-contract cases."""
+    rng = np.random.default_rng(2000 + case)
+    B = int(rng.integers(1, 3))
+    D = int(rng.choice([64, 128]))
+    dtype = str(rng.choice(["fp16", "bf16"]))
+    causal = bool(rng.integers(0, 2))
+    sigma = float(rng.choice([1.0, 2.0, 3.0]))
+    split_kv = bool(rng.integers(0, 2))
+    kind = int(rng.integers(0, 3))
+    if kind == 0:    # 0.75 to 2 causal q-tiles per CU and its neighbours
+        N, H = int(rng.integers(1500, 4200)), int(rng.choice([4, 6, 8, 12, 16]))
+    elif kind == 1:  # 8-wave non-causal range, few heads
+        N, H = int(rng.integers(2048, 5000)), int(rng.integers(1, 4))
+    else:
+        N, H = int(rng.integers(700, 2000)), int(rng.integers(4, 20))
+    _note(f"case random grid#{case}: B={B} H={H} N={N} D={D} {dtype} causal={causal} "
+          f"sigma={sigma} split_kv={split_kv}")
+    q, k, v = make_qkv(B, H, N, D, dtype, seed=case_seed(6000 + case), qk_sigma=sigma,
+                       device="cpu")
+    scale = 1.0 / math.sqrt(D)
+    o, lse = _fwd(fa, q.to(DEV), k.to(DEV), v.to(DEV), causal, split_kv=split_kv)
+    heads, sel_bh, sel_row = _sample_rows(N, B * H, rng, n_random=24)
+    qn, kn, vn = (to_np32(t.reshape(1, B * H, N, D)) for t in (q, k, v))
+    ref_o, ref_lse = oracle.attn_rows_f64(qn, kn, vn, scale, causal, sel_bh, sel_row)
+    emu_o, _ = oracle.kernel_numerics_rows(qn, kn, vn, scale, causal, sel_bh, sel_row,
+                                           oracle.BF16 if dtype == "bf16" else oracle.F16)
+    got_o = to_np32(o.reshape(B * H, N, D))[sel_bh, sel_row]
+    got_lse = to_np32(lse.reshape(B * H, N))[sel_bh, sel_row]
+    mx, mean = err_stats(got_o, ref_o)
+    emx, emean = err_stats(emu_o, ref_o)
+    lse_err = float(np.abs(got_lse.astype(np.float64) - ref_lse).max())
+    _note(f"  sampled {len(sel_row)} rows: max_abs={mx:.3e} mean_abs={mean:.3e} "
+          f"(ref-kernel emu {emx:.3e}/{emean:.3e}) lse={lse_err:.3e}")
+    assert np.isfinite(got_o).all()
+    if dtype == "fp16":
+        assert mx <= MAX_ABS_TOL, f"max-abs {mx}"
+    assert mx <= 2 * emx + 1e-6 and mean <= 2 * emean + 1e-6
+    assert lse_err <= LSE_TOL
+
+
 @pytest.mark.parametrize("dtype", ["fp16", "bf16"])
 @pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("N", [2048, 2049, 2300])
