@@ -491,13 +491,17 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
     // ---- masking (ragged tail / causal diagonal) ----
     const bool need_mask = (kt0 + BN > N) || (CAUSAL && kt0 + BN - 1 > wrow0);
     if (need_mask) {
+      // Score (kb, i) holds key kt0 + 4g + off with the compile-time offset
+      // off = 32kb + 8(i >> 2) + (i & 3); it is masked when the key exceeds
+      // N - 1 or (causal) the row.  One per-lane limit then leaves a compare
+      // and a select per score.
+      const int last = (CAUSAL ? min(N - 1, qrow) : N - 1) - kt0 - 4 * g;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          const int key = kt0 + kb * 32 + 8 * (i >> 2) + 4 * g + (i & 3);
-          const bool masked = key >= N || (CAUSAL && key > qrow);
-          if (masked) s[kb][i] = -INFINITY;
+          const int off = kb * 32 + 8 * (i >> 2) + (i & 3);
+          if (off > last) s[kb][i] = -INFINITY;
         }
     }
 
