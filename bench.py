@@ -7,11 +7,20 @@ A step is one forward over one batch of synthetic input already resident in
 HBM: flash_attention_runtime.forward(q, k, v, o) on the headline workload C3
 (B=4, H=32, N=4096, D=128, fp16, non-causal; Q, K, V ~ N(0, 1) from seed
 1234 + 100003*2, the reference's convention in
-benchmark/python/input_data.py:11-30).  W untimed warmup steps (default 1000,
-about a second of C3: the power-limited chip's clock is still rising after
-the first hundred launches on a fresh GPU), then K steps
+benchmark/python/input_data.py:11-30).  W untimed warmup steps, then K steps
 timed by two HIP events on the stream the kernel is launched on, bracketed by
 device synchronisation.  FLOPs per step = 4*B*H*N^2*D (halved for causal).
+
+Order of the run: the CPU baseline (host only), then the cold-cache figure
+(COLD_LAUNCHES launches of the same workload on the same tensors, each after
+a 512 MiB cache flush), then the W warmup and K timed steps, with no idle gap
+between them.  On a fresh MI355X the power controller takes about 25
+back-to-back C3 launches to settle after the GPU starts from idle: the first
+launch runs at a high clock, launches 2-6 at a low one (1.2 ms instead of
+0.96 ms) and the next 20 recover step by step.  The cold-cache launches come
+first so that the timed steps measure the settled clock, which is what a
+caller issuing attention back to back sees; the JSON line reports how many
+launches of the workload preceded the timed region ("launches_before_timed").
 
 Prints one JSON line with the metric, the roofline of the kernel (MFMA bound,
 against MI355X's published dense fp16/bf16 peak of 2.5 PFLOP/s) and a CPU
@@ -74,9 +83,13 @@ def make_inputs(torch, name, device, input_mode="random"):
     return (q, k, v), causal
 
 
-def time_workload(torch, fa, name, steps, warmup, input_mode="random", split_kv=True):
-    (q, k, v), causal = make_inputs(torch, name, "cuda", input_mode)
-    o = torch.empty_like(q)
+def time_workload(torch, fa, name, steps, warmup, input_mode="random", split_kv=True,
+                  tensors=None):
+    if tensors is None:
+        (q, k, v), causal = make_inputs(torch, name, "cuda", input_mode)
+        o = torch.empty_like(q)
+    else:
+        q, k, v, o, causal = tensors
     for _ in range(warmup):
         fa.forward(q, k, v, o, causal=causal, split_kv=split_kv)
     stream = torch.cuda.current_stream()
@@ -132,13 +145,15 @@ def gemm_ceiling(torch, steps, warmup):
                 del a, b, c
 
 
-def time_cold(torch, fa, name, steps, input_mode="random"):
+COLD_LAUNCHES = 50
+
+
+def time_cold(torch, fa, q, k, v, o, causal, steps):
     """Per-launch time with the last-level caches flushed before every launch
     (a 512 MiB write; MI355X's L2 + MALL hold 256 MiB), each launch bracketed
     by its own HIP events (benchmark_pybind.py:135-176 does the same with
-    100 MiB)."""
-    (q, k, v), causal = make_inputs(torch, name, "cuda", input_mode)
-    o = torch.empty_like(q)
+    100 MiB).  Returns the median time, its TFLOP/s and the number of
+    launches made (steps + 1)."""
     flush = torch.empty(512 << 20, dtype=torch.int8, device="cuda")
     fa.forward(q, k, v, o, causal=causal)
     times = []
@@ -154,7 +169,7 @@ def time_cold(torch, fa, name, steps, input_mode="random"):
     times.sort()
     ms = times[len(times) // 2]
     B, H, N, D = q.shape
-    return ms, flops(B, H, N, D, causal) / (ms * 1e-3) / 1e12
+    return ms, flops(B, H, N, D, causal) / (ms * 1e-3) / 1e12, steps + 1
 
 
 def cpu_baseline(name, budget_s=15.0):
@@ -245,7 +260,7 @@ def main():
     ap = argparse.ArgumentParser(description="MI355X FlashAttention-2 forward benchmark")
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
-    ap.add_argument("--warmup", type=int, default=1000)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="C3", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--all", action="store_true", help="also time every config (stderr table)")
@@ -315,7 +330,15 @@ def main():
 
     name = args.workload
     B, H, N, D, dtype, causal, sigma, case = WORKLOADS[name]
-    ms, tflops, wall_ms = time_workload(torch, fa, name, args.steps, args.warmup, args.input_mode)
+    # Host-only baselines first: the GPU idles meanwhile, and nothing idles it
+    # between the cold-cache launches and the timed steps.
+    cpu = None if args.no_cpu_baseline else cpu_baseline(name)
+    cpu_torch = None if args.no_cpu_baseline else cpu_torch_baseline(name)
+    (q, k, v), _ = make_inputs(torch, name, "cuda", args.input_mode)
+    o = torch.empty_like(q)
+    cold_ms, cold_tflops, n_cold = time_cold(torch, fa, q, k, v, o, causal, COLD_LAUNCHES)
+    ms, tflops, wall_ms = time_workload(torch, fa, name, args.steps, args.warmup,
+                                        tensors=(q, k, v, o, causal))
     info = fa.device_info(0)
 
     traffic = None
@@ -331,9 +354,6 @@ def main():
             print(f"{wn:5s} {wms:9.4f} {wtf:9.1f} {100 * wtf / PEAK_FP16_TFLOPS:6.1f}%",
                   file=sys.stderr, flush=True)
 
-    cold_ms, cold_tflops = time_cold(torch, fa, name, 20, args.input_mode)
-    cpu = None if args.no_cpu_baseline else cpu_baseline(name)
-    cpu_torch = None if args.no_cpu_baseline else cpu_torch_baseline(name)
 
     line = {
         "metric": "fwd TFLOPS + % of FP16 MFMA peak, B4 H32 N4096 D128 fp16 (1 GPU)",
@@ -367,7 +387,9 @@ def main():
         "cpu_baseline": cpu,
         "cpu_baseline_torch": cpu_torch,
         "cold": {"ms_per_step": round(cold_ms, 5), "tflops": round(cold_tflops, 2),
-                 "note": "median of 20 launches, each after a 512 MiB cache flush"},
+                 "note": f"median of {COLD_LAUNCHES} launches, each after a 512 MiB cache flush, "
+                         "run before the warmup steps"},
+        "launches_before_timed": n_cold + args.warmup,
         "device": {k: info[k] for k in ("arch", "compute_units", "clock_khz",
                                         "fp16_dense_peak_tflops")},
         "wall_ms_timed_region": round(wall_ms, 2),

@@ -190,9 +190,13 @@ fa_status fa_fwd_ws_timed(const fa_fwd_params* p, void* workspace, uint64_t work
  * workspace: allocates nothing (no hipMalloc, no allocating library call).
  * No counterpart in the reference; it is for callers that cannot allocate
  * device memory (code under HIP graph capture, tight serving loops, harnesses
- * that forbid allocation).  The array (FA_SCRATCH_BYTES per device) is
- * reserved on every device the library runs on until the process ends; its
- * address is looked up on the first call per device.  A problem whose
+ * that forbid allocation).  The array (FA_SCRATCH_BYTES per device) is part
+ * of the library's device code object: it is reserved when the first launch
+ * of any entry point of the library on a device loads that code object there
+ * (as every HIP module's globals are), and held until the process ends; its
+ * address is looked up on the first fa_fwd_scratch call per device.  A caller
+ * that must see no device allocation at all from this call makes one launch of
+ * the library on that device beforehand (any entry point).  A problem whose
  * split-KV plan needs more than FA_SCRATCH_BYTES is rejected with
  * FA_ERR_UNSUPPORTED and nothing is launched.  Every call on one device
  * shares that device's array, which keeps the last call's contents: calls

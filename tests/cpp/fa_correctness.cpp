@@ -1,9 +1,10 @@
 // fa_correctness — C++ correctness check of the forward through the C ABI.
 //
 // TEST INFRASTRUCTURE: built by tests/cpp/build_cpp.py into tests/cpp/ and
-// run by tests/test_gpu_cpp_correctness.py; never linked into
-// libfa_mi355x.so.  It links the library (include/fa_mi355x.h) and the CPU
-// oracle (oracle/liboracle.so) as the checker.
+// run by tests/test_gpu_cpp_tools.py::test_cpp_correctness_executable;
+// never linked into libfa_mi355x.so.  It links the library
+// (include/fa_mi355x.h) and the CPU oracle (oracle/liboracle.so) as the
+// checker.
 //
 // Replaces the reference's benchmark/cpp/correctness_v6.cu:106-217.  Case 0
 // is that file's case: B=1 H=1 N=64 D=128 fp16, non-causal, inputs

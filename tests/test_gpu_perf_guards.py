@@ -8,7 +8,9 @@ workgroup; the kernel instead leaves the optimistic pass after the first
 tile.  A regression there doubles the time on such inputs while every
 parity test still passes, so it is guarded here by timing: wide-score
 inputs may cost a little more than N(0, 1) inputs (the checked pass), never
-close to twice as much.
+close to twice as much.  Both timings come from the same box in the same
+process, so the bar (1.5x; measured 1.03-1.07x, the regression it guards
+against 1.9x) does not depend on which MI355X runs it.
 """
 from __future__ import annotations
 
@@ -51,4 +53,4 @@ def test_wide_scores_do_not_double_the_time(fa, causal, N, sigma):
     t3 = min(_time(fa, q3, k3, v3, causal) for _ in range(2))
     print(f"  N(0,1): {t1:.4f} ms   N(0,{sigma}^2): {t3:.4f} ms   ratio {t3 / t1:.3f}",
           flush=True)
-    assert t3 / t1 < 1.3
+    assert t3 / t1 < 1.5

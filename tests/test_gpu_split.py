@@ -193,6 +193,35 @@ def test_split_wide_workgroup_sampled_rows(fa, oracle, lib, cus, causal, N, H):
     assert lse_err <= LSE_TOL
 
 
+@pytest.mark.parametrize("B,H,N,dtype", [(1, 4, 8192, "fp16"), (1, 2, 8192, "bf16")],
+                         ids=["S2-fp16", "S4-bf16"])
+def test_split_full_tensor_through_fa_fwd_ws(fa, oracle, lib, cus, B, H, N, dtype):
+    """The bench's few-head causal shapes S2 and S4 (N = 8192, BASELINE-sized
+    rows), called through the C ABI's fa_fwd_ws with a workspace of exactly
+    fa_fwd_workspace_size bytes: the plan must split (chunks and the merge
+    kernel run), and every element of O and the LSE is checked against the
+    fp64 oracle and the reference-kernel emulator at the contract bars
+    (benchmark/cpp/correctness_v6.cu:74-104 is the reference's gate)."""
+    _note(f"case split full tensor {B}x{H}x{N}x128 {dtype} causal via fa_fwd_ws")
+    D = 128
+    q, k, v = make_qkv(B, H, N, D, dtype, seed=case_seed(907 + H), device=DEV)
+    pl = _assert_split(lib, cus, q, k, v, True)
+    o = torch.full_like(q, float("nan"))
+    lse = torch.full((B, H, N), float("nan"), dtype=torch.float32, device=DEV)
+    p = A.params_from_tensors(q, k, v, o, lse, True)
+    need = ctypes.c_uint64(0)
+    assert lib.fa_fwd_workspace_size(ctypes.byref(p), ctypes.byref(need)) == A.FA_OK
+    assert need.value == pl.workspace_bytes > 0
+    ws = torch.empty(need.value, dtype=torch.uint8, device=DEV)
+    assert lib.fa_fwd_ws(ctypes.byref(p), ctypes.c_void_p(ws.data_ptr()), need.value,
+                         _stream()) == A.FA_OK, lib.fa_last_error()
+    torch.cuda.synchronize()
+    _check_against_oracle(oracle, q, k, v, o, lse, True, 1.0 / math.sqrt(D), dtype)
+    o1, lse1 = fa.forward(q, k, v, causal=True, return_lse=True, split_kv=False)
+    torch.cuda.synchronize()
+    _vs_unsplit(o, lse, o1, lse1, dtype)
+
+
 def test_split_strided_output_in_padded_buffer(fa, oracle, lib, cus):
     """BNHD views with a padded seq stride for Q, K, V and O; O lives inside a
     NaN-filled buffer: the split kernel and the merge write exactly the view."""
