@@ -3,6 +3,8 @@
 Outputs (next to the Python package, so they travel with the repository):
   flash_attention_runtime/libfa_mi355x.so   HIP kernels + C ABI (hipcc, gfx950)
   flash_attention_runtime/libfa_mi355x_poison.so   the same with LDS poisoning (tests only)
+  flash_attention_runtime/libfa_mi355x_mfma32.so   the same with the 32x32x16 MFMA form of the
+                                                   fp16 8-wave kernel (tests and counters only)
   flash_attention_runtime/_C<EXT_SUFFIX>     torch/pybind binding over the C ABI
   flash_attention_runtime/fa_profile         C++ benchmark CLI over the C ABI
   flash_attention_runtime/fa_device_query    device description CLI over the C ABI
@@ -69,7 +71,11 @@ def build_hip_library(jobs: int) -> list[str]:
     shared library libfa_mi355x.so.  The kernel source is compiled a second
     time with -DFA_LDS_POISON into the debug library
     libfa_mi355x_poison.so (same ABI; staged LDS is filled with NaN before
-    every staging write), which only the tests load."""
+    every staging write), and a third time with -DFA_MFMA32 into
+    libfa_mi355x_mfma32.so (same ABI; fp16 non-causal problems of the
+    8-wave range run the 32x32x16 MFMA form of the kernel instead of the
+    16x16x32 one), which only the tests and the counter comparison of the
+    MFMA shapes load."""
     os.makedirs(BUILD_DIR, exist_ok=True)
     hipcc = _hipcc()
     kernel = os.path.join(CSRC, "fa_fwd_kernel.hip")
@@ -85,11 +91,14 @@ def build_hip_library(jobs: int) -> list[str]:
                      "-o", obj_of(src)])
     cmds.append([hipcc, *HIP_FLAGS, "-DFA_LDS_POISON", "-I", INCLUDE, "-I", CSRC, "-x", "hip",
                  "-c", kernel, "-o", obj_of(kernel, ".poison")])
+    cmds.append([hipcc, *HIP_FLAGS, "-DFA_MFMA32", "-I", INCLUDE, "-I", CSRC, "-x", "hip",
+                 "-c", kernel, "-o", obj_of(kernel, ".mfma32")])
     with ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
         list(ex.map(_run, cmds))
     libs = []
     for name, kobj in (("libfa_mi355x.so", obj_of(kernel)),
-                       ("libfa_mi355x_poison.so", obj_of(kernel, ".poison"))):
+                       ("libfa_mi355x_poison.so", obj_of(kernel, ".poison")),
+                       ("libfa_mi355x_mfma32.so", obj_of(kernel, ".mfma32"))):
         lib = os.path.join(OUT_DIR, name)
         _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", kobj,
               *[obj_of(h) for h in host], "-o", lib + ".tmp"])

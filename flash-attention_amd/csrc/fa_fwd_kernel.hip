@@ -970,6 +970,9 @@ hipError_t launch_one(const KernelArgs& a, hipStream_t stream) {
   }
 }
 
+// The 16x16x32 MFMA kernel of fp16 non-causal problems in the 8-wave range.
+#include "fa_fwd_mf16.inc"
+
 template <int D, bool BF16>
 hipError_t launch_causal(const KernelArgs& a, hipStream_t stream) {
   if (a.causal) {
@@ -987,6 +990,23 @@ hipError_t launch_causal(const KernelArgs& a, hipStream_t stream) {
   // limited there and the saved data movement buys clock (measured +3 % at
   // N = 4096).  Shorter or causal problems keep 4 waves and two workgroups
   // per CU, which fill the machine better.
+  // fp16 at D = 128: the 16x16x32 MFMA form (fa_fwd_mf16_kernel; +8 % at
+  // B4 H32 N4096 over this kernel's 32x32x16 form on the same box: it runs
+  // 6 % more cycles at a 15 % higher clock).  The test-only build
+  // libfa_mi355x_mfma32.so (-DFA_MFMA32) keeps the 32x32x16 form here, for
+  // the counter comparison of the two shapes.
+#ifndef FA_MFMA32
+  if constexpr (D == 128 && !BF16)
+    if (a.seq_len >= kWideMinSeq && a.split.n_items == 0) {
+      KernelArgs args = a;
+      args.n_qblocks = (a.seq_len + 255) / 256;
+      const int64_t total = (int64_t)args.batch * args.heads * args.n_qblocks;
+      if (total > 0x7fffffff) return hipErrorInvalidValue;
+      void* kargs[] = {&args};
+      return hipLaunchKernel(reinterpret_cast<const void*>(&fa_fwd_mf16_kernel), dim3((unsigned)total),
+                             dim3(512), kargs, 0, stream);
+    }
+#endif
   if (a.seq_len >= kWideMinSeq) return launch_one<D, BF16, false, 8>(a, stream);
   return launch_one<D, BF16, false, 4>(a, stream);
 }

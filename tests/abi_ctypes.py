@@ -20,6 +20,9 @@ LIB_PATH = os.environ.get("FA_MI355X_LIB") or os.path.join(
 # The LDS-poison debug build of the same library (flash-attention_amd/build.py).
 POISON_LIB_PATH = os.path.join(
     REPO_ROOT, "flash-attention_amd", "flash_attention_runtime", "libfa_mi355x_poison.so")
+# The build whose fp16 8-wave non-causal kernel keeps the 32x32x16 MFMA form.
+MFMA32_LIB_PATH = os.path.join(
+    REPO_ROOT, "flash-attention_amd", "flash_attention_runtime", "libfa_mi355x_mfma32.so")
 
 FA_OK, FA_ERR_NULL, FA_ERR_DTYPE, FA_ERR_SHAPE, FA_ERR_HEADDIM, FA_ERR_STRIDE, \
     FA_ERR_UNSUPPORTED, FA_ERR_HIP, FA_ERR_ARG = range(9)

@@ -92,6 +92,16 @@ def test_poison_build_exports_the_same_abi():
         assert hasattr(L, n) and n in exported, n
 
 
+def test_mfma32_build_exports_the_same_abi():
+    """The 32x32x16-MFMA test library exports the same ABI and loads on a
+    host without a GPU."""
+    if not os.path.exists(A.MFMA32_LIB_PATH):
+        pytest.skip("run build() first: no 32x32x16 library")
+    L = A.load(A.MFMA32_LIB_PATH)
+    for n in A.declared_functions():
+        assert hasattr(L, n), n
+
+
 def test_status_enum_matches_header():
     text = open(A.HEADER).read()
     import re

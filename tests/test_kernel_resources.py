@@ -68,6 +68,10 @@ def test_forward_variants_fit_two_waves_per_simd(device_asm):
     assert len(pair) == 4 and all(args[n][2] == "1" and args[n][3] == "8" and args[n][4] == "0"
                                   for n in pair)
     assert sum("fa_merge_kernel" in n for n, _ in kernels) == 4
+    mf16 = [(n, f) for n, f in kernels if "fa_fwd_mf16_kernel" in n]
+    assert len(mf16) == 1
+    # the 16x16x32 kernel: the same 4-tile K/V ring at D = 128, and its flag
+    assert int(mf16[0][1]["group_segment_fixed_size"]) == 4 * 64 * 2 * 128 + 4
     for name, f in kernels:
         assert int(f["private_segment_fixed_size"]) == 0, (name, "scratch")
         assert int(f["vgpr_spill_count"]) == 0, (name, "VGPR spills")
