@@ -970,45 +970,53 @@ hipError_t launch_one(const KernelArgs& a, hipStream_t stream) {
   }
 }
 
-// The 16x16x32 MFMA kernel of fp16 non-causal problems in the 8-wave range.
-#include "fa_fwd_mf16.inc"
+// The 16x16x32 MFMA kernel of every unsplit launch outside pair mode.
+#include "fa_fwd16.inc"
+
+// fa_fwd16_kernel where it runs (see launch_causal), else fa_fwd_kernel.
+template <int D, bool BF16, bool CAUSAL, int NW>
+hipError_t launch_pick(const KernelArgs& a, hipStream_t stream, bool plain) {
+#ifndef FA_MFMA32
+  if constexpr (D == 128)
+    if (plain) return launch16<D, BF16, CAUSAL, NW>(a, stream);
+#endif
+  return launch_one<D, BF16, CAUSAL, NW>(a, stream);
+}
 
 template <int D, bool BF16>
 hipError_t launch_causal(const KernelArgs& a, hipStream_t stream) {
+  // D = 128 launches without split-KV chunks or pair mode (plain order or an
+  // XCD placement table) run fa_fwd16_kernel, the 16x16x32 MFMA form; split
+  // chunks, pair mode and D = 64 run this file's 32x32x16 kernel.  Measured
+  // on two boxes, 16x16x32 against 32x32x16: +2...+8 % at B4 H32 N4096 fp16,
+  // +2...+4 % at bf16 causal B2 H32 N8192, +0...+5 % on fp16 causal
+  // B1 H16 N16384; at D = 64 with 4 waves (B4 H16 N1024) -1...-5 %: there the
+  // softmax's VALU work already matches the MFMA work, and the 16x16 shape
+  // takes twice the MFMA issue slots.  The test-only build
+  // libfa_mi355x_mfma32.so (-DFA_MFMA32) runs the 32x32x16 kernel
+  // everywhere, for the counter comparison of the two shapes.
+  const bool plain =
+      a.split.n_items == 0 || (a.split.xcd_heads > 0 && a.split.n_merge == 0);
   if (a.causal) {
     // Long causal fp16 rows: 8-wave workgroups (+1.4 % at B1 H16 N16384,
     // +4 % with the matrix-core row sums they enable); bf16 measured neutral
     // and short problems lose (-11 % at N = 3000: fewer, longer workgroups).
     if constexpr (!BF16)
-      if (a.seq_len >= kWideCausalMinSeq) return launch_one<D, BF16, true, 8>(a, stream);
+      if (a.seq_len >= kWideCausalMinSeq)
+        return launch_pick<D, BF16, true, 8>(a, stream, plain);
     // Grids of 0.75 to 2 q-tiles per CU: pair mode (plan_split decides).
     if (a.split.pair) return launch_one<D, BF16, true, 8, true>(a, stream);
-    return launch_one<D, BF16, true, 4>(a, stream);
+    return launch_pick<D, BF16, true, 4>(a, stream, plain);
   }
   // Long non-causal rows: 8 waves (BM = 256) per workgroup, one workgroup
   // per CU, halve the L2->LDS tile traffic per flop; the chip is power
   // limited there and the saved data movement buys clock (measured +3 % at
   // N = 4096).  Shorter or causal problems keep 4 waves and two workgroups
   // per CU, which fill the machine better.
-  // fp16 at D = 128: the 16x16x32 MFMA form (fa_fwd_mf16_kernel; +8 % at
-  // B4 H32 N4096 over this kernel's 32x32x16 form on the same box: it runs
-  // 6 % more cycles at a 15 % higher clock).  The test-only build
-  // libfa_mi355x_mfma32.so (-DFA_MFMA32) keeps the 32x32x16 form here, for
-  // the counter comparison of the two shapes.
-#ifndef FA_MFMA32
-  if constexpr (D == 128 && !BF16)
-    if (a.seq_len >= kWideMinSeq && a.split.n_items == 0) {
-      KernelArgs args = a;
-      args.n_qblocks = (a.seq_len + 255) / 256;
-      const int64_t total = (int64_t)args.batch * args.heads * args.n_qblocks;
-      if (total > 0x7fffffff) return hipErrorInvalidValue;
-      void* kargs[] = {&args};
-      return hipLaunchKernel(reinterpret_cast<const void*>(&fa_fwd_mf16_kernel), dim3((unsigned)total),
-                             dim3(512), kargs, 0, stream);
-    }
-#endif
-  if (a.seq_len >= kWideMinSeq) return launch_one<D, BF16, false, 8>(a, stream);
-  return launch_one<D, BF16, false, 4>(a, stream);
+  const bool plain_nc = a.split.n_items == 0;
+  if (a.seq_len >= kWideMinSeq)
+    return launch_pick<D, BF16, false, 8>(a, stream, plain_nc);
+  return launch_pick<D, BF16, false, 4>(a, stream, plain_nc);
 }
 
 }  // namespace

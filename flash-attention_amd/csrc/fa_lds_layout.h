@@ -96,6 +96,63 @@ FA_LAYOUT_FN int v_read_offset(int ch, int hf, int db, int lane) {
   return key * T::ROWB + (((col >> 3) ^ T::swz_v(key)) << 4) + (col & 7) * 2;
 }
 
+// ---- Layout of the 16x16x32 kernel (fa_fwd16_kernel) ----
+// K tiles keep Tile<D>::swz_k: its 16-byte reads cover 16 consecutive keys
+// (lanes l % 16) of one chunk, which the swizzle spreads over all 64 banks.
+// V tiles get their own chunk swizzle: a 32-lane pass of the transposing
+// read covers 8 consecutive keys x 32 bytes (two chunks of head dims), so
+// each key's chunk pair is XORed with a distinct even index.  Both swizzles
+// only depend on key % 16, so key blocks 16 apart share the per-lane offsets.
+#ifndef FA_LDS_SWZ_V16_CLEAR
+#define FA_LDS_SWZ_V16_CLEAR 0
+#endif
+template <int D>
+struct Tile16 {
+  static FA_LAYOUT_FN int swz_k(int key) { return Tile<D>::swz_k(key); }
+  static FA_LAYOUT_FN int swz_v(int key) {
+    return (D == 128 ? ((key & 7) << 1) : (((key >> 1) & 3) << 1)) & ~FA_LDS_SWZ_V16_CLEAR;
+  }
+};
+
+// DMA placement (as dma_slot) with the 16x16 kernel's V swizzle.
+template <int D, int NW, bool IS_V>
+FA_LAYOUT_FN void dma_slot16(int wave, int it, int lane, int& r, int& c) {
+  using T = Tile<D>;
+  constexpr int ITERS = T::BYTES / (1024 * NW);
+  const int off = (wave * ITERS + it) * 1024 + lane * 16;
+  r = off / T::ROWB;
+  const int pc = (off % T::ROWB) / 16;
+  c = pc ^ (IS_V ? Tile16<D>::swz_v(r) : Tile16<D>::swz_k(r));
+}
+
+// Byte offset within a K tile of the 16 bytes lane `lane` reads (one
+// ds_read_b128) as the A operand of the 16x16x32 S^T product for key block
+// kb (16 keys) and k-step st (32 head dims): key 16kb + lane % 16, head dims
+// [32st + 8(lane / 16), +8).  Key block kb adds kb * 16 * ROWB to block 0.
+template <int D>
+FA_LAYOUT_FN int k16_read_offset(int kb, int st, int lane) {
+  using T = Tile<D>;
+  const int key = 16 * kb + (lane & 15);
+  const int chunk = 4 * st + (lane >> 4);
+  return key * T::ROWB + ((chunk ^ Tile16<D>::swz_k(key)) << 4);
+}
+
+// Byte offset within a V tile of the 8 bytes lane `lane` addresses with one
+// ds_read_b64_tr_b16 for the V^T operand of 32-key chunk ch, half h and
+// 16-wide head-dim block db: row key = 32ch + 16h + 4(lane / 16) +
+// (lane % 16) / 4, columns 16db + 4(lane % 4) .. +3 (the transposing read
+// hands lane i of each 16-lane group element i % 4 of the words addressed
+// by lanes 4e + i / 4, so lane i of group g receives V[32ch + 16h + 4g + e]
+// [16db + i] for e = 0..3).  Chunks and halves add (32ch + 16h) * ROWB.
+template <int D>
+FA_LAYOUT_FN int v16_read_offset(int ch, int h, int db, int lane) {
+  using T = Tile<D>;
+  const int l16 = lane & 15, g4 = lane >> 4;
+  const int key = 32 * ch + 16 * h + 4 * g4 + (l16 >> 2);
+  const int col = 16 * db + 4 * (l16 & 3);
+  return key * T::ROWB + (((col >> 3) ^ Tile16<D>::swz_v(key)) << 4) + (col & 7) * 2;
+}
+
 // Row tiles: 32 rows of `rowb` bytes (rowb = 128, 256 or 512) that a wave
 // stages on its own, Q for its MFMA operands (4-wave workgroups) and O or
 // the fp32 split partials on their way out.  Row r's 16-byte chunk c sits at
