@@ -172,6 +172,44 @@ def time_cold(torch, fa, q, k, v, o, causal, steps):
     return ms, flops(B, H, N, D, causal) / (ms * 1e-3) / 1e12, steps + 1
 
 
+SHAPE_LIBS = {
+    "product": os.path.join(REPO_ROOT, "flash-attention_amd", "flash_attention_runtime", "libfa_mi355x.so"),
+    "mfma32": os.path.join(REPO_ROOT, "flash-attention_amd", "flash_attention_runtime",
+                           "libfa_mi355x_mfma32.so"),
+}
+
+
+def time_abi(torch, lib_name, name, steps, warmup, rounds):
+    """Times one workload through the C ABI (fa_fwd) of the product library
+    (D = 128 on the 16x16x32 MFMA kernel) or of the test-only build that keeps
+    the 32x32x16 form everywhere (libfa_mi355x_mfma32.so): W launches, then
+    `rounds` groups of K launches, each timed by HIP events.  Returns the
+    per-launch ms of each group."""
+    import ctypes
+
+    sys.path.insert(0, os.path.join(REPO_ROOT, "tests"))
+    import abi_ctypes as A
+
+    lib = A.load(SHAPE_LIBS[lib_name])
+    (q, k, v), causal = make_inputs(torch, name, "cuda")
+    o = torch.empty_like(q)
+    p = A.params_from_tensors(q, k, v, o, None, causal)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    for _ in range(warmup):
+        assert lib.fa_fwd(ctypes.byref(p), stream) == 0, lib.fa_last_error()
+    out = []
+    for _ in range(rounds):
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(steps):
+            lib.fa_fwd(ctypes.byref(p), stream)
+        b.record()
+        torch.cuda.synchronize()
+        out.append(a.elapsed_time(b) / steps)
+    return out
+
+
 def cpu_baseline(name, budget_s=15.0):
     """Times the reference CPU path (oracle_ref_online_f32: fp32 online softmax
     with expf, one query row at a time) on the first rows of the workload, on
@@ -272,6 +310,12 @@ def main():
     ap.add_argument("--gemm-ceiling", action="store_true",
                     help="instead of attention, time torch.matmul (hipBLASLt) fp16/bf16 GEMMs on "
                          "N(0,1) and on constant data: the data-dependent MFMA ceiling of the box")
+    ap.add_argument("--mfma-shapes", action="store_true",
+                    help="instead of the metric, time --workload (or C3 and C4) through the C ABI of "
+                         "the product library and of the 32x32x16 build (--shape-lib picks one), "
+                         "alternating (stderr table)")
+    ap.add_argument("--shape-lib", choices=sorted(SHAPE_LIBS), default=None,
+                    help="with --mfma-shapes: time only this library (for counter runs)")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="instead of attention, time a plain device copy of this many MiB "
                          "(calibrates the FETCH_SIZE / WRITE_SIZE counters)")
@@ -312,6 +356,24 @@ def main():
 
     if args.gemm_ceiling:
         gemm_ceiling(torch, args.steps, args.warmup)
+        return
+
+    if args.mfma_shapes:
+        libs = [args.shape_lib] if args.shape_lib else ["mfma32", "product"]
+        names = [args.workload] if "--workload" in sys.argv else ["C3", "C4"]
+        print(f"{'cfg':5s} {'library':8s} {'ms per launch (rounds)':>40s} {'best TFLOPS':>12s}",
+              file=sys.stderr, flush=True)
+        for wn in names:
+            B, H, N, D, dtype, causal, _, _ = WORKLOADS[wn]
+            res = {ln: [] for ln in libs}
+            for _ in range(2):  # alternate the libraries, twice
+                for ln in libs:
+                    res[ln] += time_abi(torch, ln, wn, args.steps, args.warmup, 2)
+            for ln in libs:
+                best = min(res[ln])
+                print(f"{wn:5s} {ln:8s} {' '.join(f'{t:.4f}' for t in res[ln]):>40s} "
+                      f"{flops(B, H, N, D, causal) / (best * 1e-3) / 1e12:12.1f}",
+                      file=sys.stderr, flush=True)
         return
 
     if args.split_table:

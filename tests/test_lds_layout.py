@@ -18,6 +18,10 @@ For D in {64, 128} and workgroups of 4 and 8 waves:
   the current layout (profiles/fa_fwd_C3_counters.md);
 - the bank check sees a dropped swizzle bit: a copy built with one bit of the
   K or V swizzle cleared still reads what it wrote, but conflicts;
+- the same four checks for the layout of the 16x16x32 kernel (lds::Tile16,
+  dma_slot16, k16_read_offset, v16_read_offset: its K reads cover 16 keys x
+  one chunk per 16-lane group, its V^T reads 8 keys x 32 bytes per 32-lane
+  pass), against that kernel's MFMA lane maps;
 - the row tiles a wave stages on its own (Q operands, the O and split-partial
   stores) are bijections whose 16-byte writes and reads are conflict free, a
   copy with a row-swizzle bit cleared conflicts, and 8-byte writes would
@@ -54,6 +58,9 @@ def _build(out_dir, defines=()):
     lib.fa_lds_dma_map.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ip, ip]
     lib.fa_lds_k_reads.argtypes = [ctypes.c_int, ip]
     lib.fa_lds_v_reads.argtypes = [ctypes.c_int, ip]
+    lib.fa_lds_dma_map16.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ip, ip]
+    lib.fa_lds_k16_reads.argtypes = [ctypes.c_int, ip]
+    lib.fa_lds_v16_reads.argtypes = [ctypes.c_int, ip]
     return lib
 
 
@@ -191,6 +198,112 @@ def test_dropped_swizzle_bit_is_detected(tmp_path, D, k_clear, v_clear):
         assert kc > 0, "a dropped K swizzle bit went unnoticed"
     if v_clear:
         assert vc > 0, "a dropped V swizzle bit went unnoticed"
+
+
+# ---- the 16x16x32 kernel's layout (lds::Tile16) ----
+
+def _dma_slots16(lib, D, NW, is_v):
+    rowb = 2 * D
+    n = 64 * rowb // 16
+    r = np.empty(n, np.int32)
+    c = np.empty(n, np.int32)
+    assert lib.fa_lds_dma_map16(D, NW, int(is_v), _ptr(r), _ptr(c)) == n
+    slot = np.full((64, rowb // 16), -1, np.int64)
+    slot[r, c] = np.arange(n, dtype=np.int64) * 16
+    return slot, r, c
+
+
+def _k16_reads(lib, D):
+    off = np.empty(4 * (D // 32) * 64, np.int32)
+    assert lib.fa_lds_k16_reads(D, _ptr(off)) == off.size
+    return off.reshape(4, D // 32, 64).astype(np.int64)
+
+
+def _v16_reads(lib, D):
+    off = np.empty(2 * 2 * (D // 16) * 64, np.int32)
+    assert lib.fa_lds_v16_reads(D, _ptr(off)) == off.size
+    return off.reshape(2, 2, D // 16, 64).astype(np.int64)
+
+
+@pytest.mark.parametrize("D,NW", CASES)
+@pytest.mark.parametrize("is_v", [False, True], ids=["K", "V"])
+def test_dma16_is_a_bijection_onto_the_tile(lib, D, NW, is_v):
+    slot, r, c = _dma_slots16(lib, D, NW, is_v)
+    assert (slot >= 0).all()
+    pairs = r.astype(np.int64) * (2 * D // 16) + c
+    assert np.unique(pairs).size == pairs.size
+
+
+@pytest.mark.parametrize("D,NW", CASES)
+def test_k16_reads_find_the_staged_keys(lib, D, NW):
+    slot, _, _ = _dma_slots16(lib, D, NW, False)
+    off = _k16_reads(lib, D)
+    lane = np.arange(64)
+    for kb in range(4):
+        for st in range(D // 32):
+            # 16x16x32 A operand: lane l supplies row l % 16 (the key) and
+            # k-elements 8(l / 16) .. +7 of k-step st (head dims 32st + ...).
+            want = slot[16 * kb + lane % 16, 4 * st + lane // 16]
+            assert np.array_equal(off[kb, st], want), (kb, st)
+            # the kernel's form: key block kb = block 0 + 16kb rows
+            assert np.array_equal(off[kb, st], off[0, st] + 16 * kb * 2 * D)
+
+
+@pytest.mark.parametrize("D,NW", CASES)
+def test_v16_reads_find_the_staged_keys(lib, D, NW):
+    """Each 16-lane group g of a transposing read hands lane i element i % 4 of
+    the words addressed by lanes 4e + i / 4 (e = 0..3), so lane i must receive
+    V[32ch + 16h + 4g + e][16db + i]: the word of lane 4e + q holds row
+    32ch + 16h + 4g + e, columns 16db + 4q .. +3."""
+    slot, _, _ = _dma_slots16(lib, D, NW, True)
+    off = _v16_reads(lib, D)
+    lane = np.arange(64)
+    l16, g = lane % 16, lane // 16
+    for ch in range(2):
+        for h in range(2):
+            for db in range(D // 16):
+                key = 32 * ch + 16 * h + 4 * g + l16 // 4
+                col = 16 * db + 4 * (l16 % 4)
+                want = slot[key, col // 8] + (col % 8) * 2
+                assert np.array_equal(off[ch, h, db], want), (ch, h, db)
+                assert np.array_equal(off[ch, h, db], off[0, 0, db] + (32 * ch + 16 * h) * 2 * D)
+                # what the receiving lanes get: lane i of group gg, element e
+                for gg in range(4):
+                    for i in range(16):
+                        for e in range(4):
+                            src = 16 * gg + 4 * e + i // 4  # the addressing lane
+                            got = off[ch, h, db][src] + (i % 4) * 2
+                            k_, c_ = 32 * ch + 16 * h + 4 * gg + e, 16 * db + i
+                            assert got == slot[k_, c_ // 8] + (c_ % 8) * 2, (ch, h, db, gg, i, e)
+
+
+def _read_conflicts16(lib, D):
+    k = _k16_reads(lib, D)
+    v = _v16_reads(lib, D)
+    kc = sum(_conflicts(k[kb, st], 16, 16) for kb in range(4) for st in range(D // 32))
+    vc = sum(_conflicts(v[ch, h, db], 8, 32)
+             for ch in range(2) for h in range(2) for db in range(D // 16))
+    return kc, vc
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_reads16_are_bank_conflict_free(lib, D):
+    assert _read_conflicts16(lib, D) == (0, 0)
+
+
+@pytest.mark.parametrize("D,v_clear", [(128, 2), (128, 4), (128, 8), (64, 2), (64, 4)])
+def test_dropped_v16_swizzle_bit_is_detected(tmp_path, D, v_clear):
+    """A 16x16 V swizzle bit cleared: the reads still find what the DMA wrote,
+    but the 32-lane passes conflict."""
+    mut = _build(str(tmp_path), (f"FA_LDS_SWZ_V16_CLEAR={v_clear}",))
+    slot, _, _ = _dma_slots16(mut, D, 4, True)
+    off = _v16_reads(mut, D)
+    lane = np.arange(64)
+    l16, g = lane % 16, lane // 16
+    key = 4 * g + l16 // 4
+    col = 4 * (l16 % 4)
+    assert np.array_equal(off[0, 0, 0], slot[key, col // 8] + (col % 8) * 2)
+    assert _read_conflicts16(mut, D)[1] > 0, "a dropped V16 swizzle bit went unnoticed"
 
 
 # ---- row tiles (lds::row_tile_offset) ----
