@@ -156,11 +156,17 @@ FA_LAYOUT_FN int v16_read_offset(int ch, int h, int db, int lane) {
 // Row tiles: 32 rows of `rowb` bytes (rowb = 128, 256 or 512) that a wave
 // stages on its own, Q for its MFMA operands (4-wave workgroups) and O or
 // the fp32 split partials on their way out.  Row r's 16-byte chunk c sits at
-// chunk position c ^ row_swz(r).  16-byte writes of one chunk per lane over
-// 32 rows and 16-byte reads of whole rows are then free of bank conflicts.
+// chunk position c ^ row_swz(r).  The writes put one chunk per lane over 32
+// rows (lane l: row l % 32); a ds_write_b128 serves 8 lanes per LDS cycle,
+// which conflict unless their chunks differ mod 128 bytes, so each aligned
+// group of 8 rows needs 8 distinct positions mod 128.  The 16-byte reads
+// serve 16 lanes per cycle over all 256 bytes of banks: whole rows, and for
+// Q one chunk of 16 consecutive rows, which at rowb = 128 needs the even
+// and the odd rows of the 16 on distinct positions.  rowb >= 256: r mod
+// the row's chunk count; rowb = 128: r ^ (r >> 3) mod 8.
 FA_LAYOUT_FN int row_swz(int r, int rowb) {
   const int nc = rowb >> 4;  // chunks per row
-  return (nc >= 16 ? (r & (nc - 1)) : ((r >> 1) & (nc - 1))) & ~FA_LDS_ROW_SWZ_CLEAR;
+  return (nc >= 16 ? (r & (nc - 1)) : ((r ^ (r >> 3)) & (nc - 1))) & ~FA_LDS_ROW_SWZ_CLEAR;
 }
 FA_LAYOUT_FN int row_tile_offset(int r, int c, int rowb) {
   return r * rowb + ((c ^ row_swz(r, rowb)) << 4);

@@ -10,12 +10,15 @@ For D in {64, 128} and workgroups of 4 and 8 waves:
   the key and head dims the MFMA lane maps require;
 - the offsets the kernel uses for key block 1 and for later V chunks/halves
   (a constant added to block 0 / chunk 0) equal the general formula;
-- no read has a bank conflict, under this model of the gfx950 LDS: 64 banks
-  of 4 bytes, a wave's read served 256 bytes at a time in lane order (16
-  lanes of a ds_read_b128, 32 lanes of a ds_read_b64_tr_b16), and two lanes
-  of one group conflict when they touch the same bank at different
-  addresses.  The model agrees with the measured SQ_LDS_BANK_CONFLICT = 0 of
-  the current layout (profiles/fa_fwd_C3_counters.md);
+- no access has a bank conflict, under this model of the gfx950 LDS: 64
+  banks of 4 bytes; ds_read_b128 serves 16 lanes (256 bytes) per cycle,
+  ds_read_b64_tr_b16 32 lanes, and ds_write_b128 8 lanes (128 bytes), whose
+  addresses conflict when they agree mod 128 bytes; within a cycle, distinct
+  dwords on one bank are served one after the other.  The model is
+  calibrated on the hardware: it reproduces the conflict cycles that
+  tests/lds/lds_bank_probe.hip measured for 31 access patterns
+  (profiles/lds_bank_probe.md), and the 65536 cycles per C2 launch of the
+  previous 128-byte row swizzle;
 - the bank check sees a dropped swizzle bit: a copy built with one bit of the
   K or V swizzle cleared still reads what it wrote, but conflicts;
 - the same four checks for the layout of the 16x16x32 kernel (lds::Tile16,
@@ -103,19 +106,40 @@ def _v_reads(lib, D):
     return off.reshape(4, 2, nd, 64).astype(np.int64)
 
 
-def _conflicts(addrs, nbytes, group):
-    """Bank conflicts of one wave-wide read: lanes served `group` at a time,
-    each lane touching `nbytes` bytes from its address.  Counts, per group,
-    the bank accesses beyond one distinct address per bank."""
+def _conflict_cycles(addrs, nbytes, lanes_per_cycle, window):
+    """Bank-conflict cycles of one wave-wide LDS instruction, the quantity
+    SQ_LDS_BANK_CONFLICT counts: the lanes are served `lanes_per_cycle` at a
+    time in lane order, each touching `nbytes` bytes from its address; within
+    one cycle, distinct dwords whose addresses agree mod `window` bytes share
+    a bank and are served one after the other, so a cycle whose fullest bank
+    holds k distinct dwords costs k - 1 extra cycles."""
+    nbanks = window // BANK_BYTES
     total = 0
-    for g0 in range(0, len(addrs), group):
+    for g0 in range(0, len(addrs), lanes_per_cycle):
         seen = {}
-        for a in addrs[g0:g0 + group]:
+        for a in addrs[g0:g0 + lanes_per_cycle]:
             for w in range(0, nbytes, BANK_BYTES):
                 word = (int(a) + w) // BANK_BYTES
-                seen.setdefault(word % BANKS, set()).add(word)
-        total += sum(len(s) - 1 for s in seen.values())
+                seen.setdefault(word % nbanks, set()).add(word)
+        total += max(len(s) for s in seen.values()) - 1
     return total
+
+
+# The instruction forms, as measured on the MI355X by tests/lds/lds_bank_probe.hip
+# (kPatterns below): ds_read_b128 serves 16 lanes (256 bytes) per cycle over
+# all 64 banks; ds_write_b128 serves 8 lanes (128 bytes) per cycle, and two of
+# them conflict when their addresses agree mod 128 bytes; ds_read_b64_tr_b16
+# serves 32 lanes (256 bytes) per cycle.
+def read128(addrs):
+    return _conflict_cycles(addrs, 16, 16, 256)
+
+
+def write128(addrs):
+    return _conflict_cycles(addrs, 16, 8, 128)
+
+
+def read_tr64(addrs):
+    return _conflict_cycles(addrs, 8, 32, 256)
 
 
 CASES = [(D, NW) for D in (64, 128) for NW in (4, 8)]
@@ -166,9 +190,8 @@ def test_v_reads_find_the_staged_keys(lib, D, NW):
 def _read_conflicts(lib, D):
     k = _k_reads(lib, D)
     v = _v_reads(lib, D)
-    kc = sum(_conflicts(k[kb, kk], 16, 16) for kb in range(2) for kk in range(D // 16))
-    vc = sum(_conflicts(v[ch, hf, db], 8, 32)
-             for ch in range(4) for hf in range(2) for db in range(D // 32))
+    kc = sum(read128(k[kb, kk]) for kb in range(2) for kk in range(D // 16))
+    vc = sum(read_tr64(v[ch, hf, db]) for ch in range(4) for hf in range(2) for db in range(D // 32))
     return kc, vc
 
 
@@ -179,7 +202,7 @@ def test_reads_are_bank_conflict_free(lib, D):
 
 def test_dma_writes_are_bank_conflict_free():
     # each DMA instruction writes 64 lanes x 16 contiguous bytes
-    assert _conflicts(np.arange(64) * 16, 16, 16) == 0
+    assert write128(np.arange(64) * 16) == 0
 
 
 @pytest.mark.parametrize("D,k_clear,v_clear", [(128, 8, 0), (128, 1, 0), (128, 0, 4),
@@ -280,9 +303,8 @@ def test_v16_reads_find_the_staged_keys(lib, D, NW):
 def _read_conflicts16(lib, D):
     k = _k16_reads(lib, D)
     v = _v16_reads(lib, D)
-    kc = sum(_conflicts(k[kb, st], 16, 16) for kb in range(4) for st in range(D // 32))
-    vc = sum(_conflicts(v[ch, h, db], 8, 32)
-             for ch in range(2) for h in range(2) for db in range(D // 16))
+    kc = sum(read128(k[kb, st]) for kb in range(4) for st in range(D // 32))
+    vc = sum(read_tr64(v[ch, h, db]) for ch in range(2) for h in range(2) for db in range(D // 16))
     return kc, vc
 
 
@@ -354,9 +376,9 @@ def _q_operand_reads(lib, rowb):
 
 def _row_conflicts(lib, rowb):
     return {
-        "writes": sum(_conflicts(a, 16, 16) for a in _chunk_writes(lib, rowb)),
-        "row_reads": sum(_conflicts(a, 16, 16) for a in _row_reads(lib, rowb)),
-        "q_reads": sum(_conflicts(a, 16, 16) for a in _q_operand_reads(lib, rowb)),
+        "writes": sum(write128(a) for a in _chunk_writes(lib, rowb)),
+        "row_reads": sum(read128(a) for a in _row_reads(lib, rowb)),
+        "q_reads": sum(read128(a) for a in _q_operand_reads(lib, rowb)),
     }
 
 
@@ -371,7 +393,7 @@ def _dword_pass_conflicts(addrs):
     (the model that matches the hardware counter: SQ_LDS_BANK_CONFLICT was
     1048576 per C3 launch with 8-byte O-staging writes, whatever the swizzle,
     and 0 with the 16-byte ones)."""
-    return sum(_conflicts([a + 4 * d for a in addrs], 4, 64) for d in range(2))
+    return sum(_conflict_cycles([a + 4 * d for a in addrs], 4, 64, 256) for d in range(2))
 
 
 @pytest.mark.parametrize("rowb", [128, 256])
@@ -391,7 +413,9 @@ def test_eight_byte_output_writes_would_conflict(lib, rowb):
     (256, 8, "q_reads"),
     (256, 1, "writes"),
     (128, 4, "writes"),
-    (512, 8, "writes"),
+    (128, 1, "writes"),
+    (128, 2, "q_reads"),
+    (512, 4, "writes"),
 ])
 def test_dropped_row_swizzle_is_detected(tmp_path, rowb, clear, which):
     """With one row-swizzle bit cleared the tile is still a bijection but the
@@ -401,3 +425,98 @@ def test_dropped_row_swizzle_is_detected(tmp_path, rowb, clear, which):
     offs = sorted(_row_off(mut, r, c, rowb) for r in range(32) for c in range(nc))
     assert offs == list(range(0, 32 * rowb, 16))
     assert _row_conflicts(mut, rowb)[which] > 0
+
+
+# ---- calibration of the bank model on the hardware ----
+# tests/lds/lds_bank_probe.hip runs each pattern below as its own dispatch
+# (64 instructions per wave, 1024 waves) and profiles/lds_bank_probe.md holds
+# SQ_LDS_BANK_CONFLICT / SQ_INSTS_LDS for each: the conflict cycles of one
+# instruction.  The model must give the same number for every pattern.
+
+def _old_row128(r, c):
+    """The row tile of 128-byte rows before the current swizzle (chunk c of
+    row r at c ^ ((r >> 1) & 7)), which the C2 counters were measured with."""
+    return r * 128 + ((c ^ ((r >> 1) & 7)) << 4)
+
+
+def _probe_patterns(lib):
+    """(instruction form, 64 lane offsets) of each probe pattern, in the
+    probe's order (its offset_of<P>)."""
+    _row_lib(lib)
+    lane = np.arange(64)
+    l32, g = lane % 32, lane // 32
+    k64, k128 = _k_reads(lib, 64), _k_reads(lib, 128)
+    v64, v128 = _v_reads(lib, 64), _v_reads(lib, 128)
+    row = lambda rs, cs, rowb: [_row_off(lib, r, c, rowb) for r, c in zip(rs, cs)]
+    return [
+        (read128, lane * 16),
+        (read128, lane * 256),
+        (write128, [_old_row128(r, 0 + q) for r, q in zip(l32, g)]),
+        (write128, [_old_row128(r, 2 + q) for r, q in zip(l32, g)]),
+        (write128, [_old_row128(r, 4 + q) for r, q in zip(l32, g)]),
+        (write128, [_old_row128(r, 6 + q) for r, q in zip(l32, g)]),
+        (read128, [_old_row128(l // 8, l % 8) for l in lane]),
+        (read128, [_old_row128(8 + l // 8, l % 8) for l in lane]),
+        (read128, [_old_row128(r, 0 + q) for r, q in zip(l32, g)]),
+        (read128, [_old_row128(r, 2 + q) for r, q in zip(l32, g)]),
+        (write128, row(l32, g, 256)),
+        (read128, row(lane // 16, lane % 16, 256)),
+        (read128, k64[0, 0]),
+        (read128, k64[0, 1]),
+        (read_tr64, v64[0, 0, 0]),
+        (read_tr64, v64[0, 0, 1]),
+        (write128, lane * 16),
+        (write128, lane * 256),
+        (read128, k128[0, 0]),
+        (read_tr64, v128[0, 0, 0]),
+        (write128, row(l32, 2 + g, 256)),
+        (read128, row(l32, g, 256)),
+        (write128, (lane % 16) * 16 + (lane // 16) * 1024),
+        (write128, l32 * 16 + g * 8192),
+        (read128, l32 * 16 + g * 8192),
+        (write128, (lane % 8) * 16 + ((lane // 8) % 2) * 8192 + (lane // 16) * 128),
+        (write128, row(l32, g, 128)),
+        (write128, row(l32, 6 + g, 128)),
+        (read128, row(lane // 8, lane % 8, 128)),
+        (read128, row(l32, g, 128)),
+        (read128, row(l32, 6 + g, 128)),
+    ]
+
+
+# Conflict cycles per instruction measured by the probe (MI355X, ROCm 7.2).
+MEASURED_CONFLICT_CYCLES = [0, 60, 8, 8, 8, 8, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0,
+                            0, 56, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0]
+
+
+def test_bank_model_matches_the_probe(lib):
+    """The model reproduces the measured conflict cycles of every probe
+    pattern: the 16-lane, 256-byte read cycles (60 cycles when 16 lanes share
+    a bank group), the 8-lane, 128-byte write cycles (56 when 8 lanes share
+    one; 8 for the old 128-byte row tile, whose rows 2i and 2i + 1 agree mod
+    128 bytes although they differ mod 256), and zero elsewhere."""
+    pats = _probe_patterns(lib)
+    assert len(pats) == len(MEASURED_CONFLICT_CYCLES)
+    got = [form(np.asarray(addrs, np.int64)) for form, addrs in pats]
+    assert got == MEASURED_CONFLICT_CYCLES
+
+
+def test_bank_model_predicts_the_c2_count(lib):
+    """C2 (B4 H16 N1024 D64 fp16: 512 workgroups of 4 waves) counted
+    SQ_LDS_BANK_CONFLICT = 65536 per launch with the old 128-byte row
+    swizzle.  Under the model every read of that kernel is conflict-free and
+    each of a wave's 4 O-staging writes costs 8 cycles: 2048 waves x 32 =
+    65536.  The current swizzle gives 0."""
+    _row_lib(lib)
+    k, v = _k_reads(lib, 64), _v_reads(lib, 64)
+    tiles = 1024 // 64
+    reads = tiles * (sum(read128(k[kb, kk]) for kb in range(2) for kk in range(4)) +
+                     sum(read_tr64(v[ch, hf, db]) for ch in range(4) for hf in range(2)
+                         for db in range(2)))
+    lane = np.arange(64)
+    old_writes = sum(write128([_old_row128(l % 32, 2 * p + l // 32) for l in lane]) for p in range(4))
+    old_reads = sum(read128([_old_row128(j * 8 + l // 8, l % 8) for l in lane]) for j in range(4))
+    old_q = sum(read128([_old_row128(l % 32, 2 * kk + l // 32) for l in lane]) for kk in range(4))
+    waves = 4 * 16 * (1024 // 128) * 4
+    assert waves * (reads + old_writes + old_reads + old_q) == 65536
+    now = _row_conflicts(lib, 128)
+    assert waves * (reads + now["writes"] + now["row_reads"] + now["q_reads"]) == 0
