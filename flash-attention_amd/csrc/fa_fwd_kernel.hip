@@ -101,17 +101,20 @@ using lds::dma_slot;
 // from the row max only when a tile's P sum (per lane, 32 keys) reaches
 // kSumLimit; every P then stays below 2^15, finite in fp16 (max 65504) and
 // far from overflow in the fp32 O and l accumulators.  When it is re-derived,
-// m moves for rows whose max exceeds it by more than kRescaleThreshold (log2
-// units), to kHeadroom log2 units above that max in the checked pass: the
-// largest p of the tile is then 2^-kHeadroom, and the scores can rise
-// 15 + kHeadroom units before the next re-derivation.  Measured same box,
-// against the offset at the row max: B1 H16 N3000 causal with Q, K ~
-// N(0, 3^2) +4.3 %, causal B2 H16 N4096 with those inputs +3.2 %, B4 H32
-// N4096 with them +1.6 %, C5 +0.7 %, bf16 causal B2 H32 N8192 +0.9 %.  The
-// cost is precision in the smallest p: fp16 p below 2^-14 are subnormal, so
-// keys more than 14 - kHeadroom units under the row max keep fewer bits.  At
-// 4 the score-jump tests stay within 1.25x the emulated reference kernel's
-// error (the bar is 2x); 8 measured 2.05x there and failed.
+// m moves for every row whose max exceeds it (the rescale that follows is
+// branch-free and multiplies every row anyway), to kHeadroom log2 units above
+// that max in the checked pass: the largest p of the tile is then
+// 2^-kHeadroom, and the scores can rise 15 + kHeadroom units before the next
+// re-derivation.  Measured same box, against moving m to the row max only for
+// rows 8 units above it: B1 H16 N3000 causal with Q, K ~ N(0, 3^2) +4.3 % for
+// the headroom and another +3.4 % for moving every row, causal B2 H16 N4096
+// with those inputs +3.2 % and +6.4 %, B4 H32 N4096 with them +1.6 % and
+// +2.0 %, C5 +0.7 % and +2.0 %, bf16 causal B2 H32 N8192 with them +0.9 % and
+// +4.2 %.  The cost of the headroom is precision in the smallest p: fp16 p
+// below 2^-14 are subnormal, so keys more than 14 - kHeadroom units under the
+// row max keep fewer bits.  At 4 the score-jump tests stay within 1.25x the
+// emulated reference kernel's error (the bar is 2x); 8 measured 2.05x there
+// and failed.
 // LDS-poison debug build (compiled with -DFA_LDS_POISON, shipped as
 // libfa_mi355x_poison.so, never the product library): every wave fills the
 // LDS bytes it is about to stage (K/V ring slots, staged Q, the output
@@ -127,7 +130,6 @@ constexpr bool kLdsPoison = false;
 #endif
 
 constexpr float kSumLimit = 32768.0f;
-constexpr float kRescaleThreshold = 8.0f;
 constexpr float kHeadroom = 4.0f;
 
 // The optimistic pass keeps the first key tile's row max as the offset for
@@ -576,9 +578,9 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
     // bounds each of its terms, and is inf or NaN if a P overflowed or
     // m = -inf), so the row max is taken only when a sum reaches the limit:
     // on the first tile of a row, or when the scores jump by more than
-    // ~15/c.  Then m moves to the row max for rows whose max exceeds it by
-    // more than kRescaleThreshold (each row that tripped the check does), O
-    // and l are rescaled, and P is recomputed (kRescaleP: rescaled).
+    // ~15/c.  Then m moves (to kHeadroom above the row max in the checked
+    // pass) for every row whose max exceeds it, O and l are rescaled, and P
+    // is recomputed (kRescaleP: rescaled).
     bool rederive = true;
     if (!kSkipFirstExp || t != t_first) {
       if constexpr (OPT) {
@@ -608,7 +610,7 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
         if (__any(!((mx - mean) * c <= kOptSpreadLimit)) && lane == 0) redo_flag = 1;
       }
       const float m_old = m_run;
-      const bool grow = (mx - m_run) * c > kRescaleThreshold;  // false for NaN (-inf - -inf)
+      const bool grow = mx > m_run;  // false when both are -inf
       const float m_new = grow ? (OPT ? mx : mx + kHeadroom / c) : m_run;
       // exp2(0) = 1 for rows that keep their offset (branch-free: also
       // covers m_run = -inf, where m_run - m_new would be NaN).
