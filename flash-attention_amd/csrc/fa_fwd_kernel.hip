@@ -55,9 +55,9 @@
 // offset m taken from the raw scores, p = exp2(s*c - m*c) with
 // c = scale*log2(e), O and l rescaled by exp2((m_old - m_new)*c), P rounded
 // to the input type with round-to-nearest-even before the PV product, O
-// normalised in fp32 and rounded to the input type.  Differences: m is an
-// offset at or below the running max, raised only when a tile's P would
-// reach 2^15 (the common factor exp2(m_max*c - m*c) cancels in O/l), so the
+// normalised in fp32 and rounded to the input type.  Differences: m is a
+// lazy offset, raised only when a tile's P sums would reach kSumLimit (the
+// common factor exp2(m_max*c - m*c) cancels in O/l), so the
 // row max is computed only on such tiles (fp16 non-causal and fp16 causal in
 // 8-wave workgroups run an optimistic pass with the offset of the first tile
 // and redo the workgroup with per-tile checks only if a P overflowed); O is
@@ -99,13 +99,13 @@ using lds::dma_slot;
 
 // Lazy exponent offset.  The offset m in p = exp2(s*c - m*c) is re-derived
 // from the row max only when a tile's P sum (per lane, 32 keys) reaches
-// kSumLimit; every P then stays below 2^15, finite in fp16 (max 65504) and
+// kSumLimit; every P then stays below it, finite in fp16 (max 65504) and
 // far from overflow in the fp32 O and l accumulators.  When it is re-derived,
 // m moves for every row whose max exceeds it (the rescale that follows is
 // branch-free and multiplies every row anyway), to kHeadroom log2 units above
 // that max in the checked pass: the largest p of the tile is then
-// 2^-kHeadroom, and the scores can rise 15 + kHeadroom units before the next
-// re-derivation.  Measured same box, against moving m to the row max only for
+// 2^-kHeadroom, and the scores can rise about 16 + kHeadroom units before the
+// next re-derivation.  Measured same box, against moving m to the row max only for
 // rows 8 units above it: B1 H16 N3000 causal with Q, K ~ N(0, 3^2) +4.3 % for
 // the headroom and another +3.4 % for moving every row, causal B2 H16 N4096
 // with those inputs +3.2 % and +6.4 %, B4 H32 N4096 with them +1.6 % and
@@ -129,7 +129,9 @@ constexpr bool kLdsPoison = true;
 constexpr bool kLdsPoison = false;
 #endif
 
-constexpr float kSumLimit = 32768.0f;
+// 15 * 2^12: below fp16's largest finite value, 65504 (+1.3 % on B1 H16 N3000
+// causal and +1.8 % on causal B2 H16 N4096 with Q, K ~ N(0, 3^2) over 2^15).
+constexpr float kSumLimit = 61440.0f;
 constexpr float kHeadroom = 4.0f;
 
 // The optimistic pass keeps the first key tile's row max as the offset for
@@ -578,9 +580,9 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
     // bounds each of its terms, and is inf or NaN if a P overflowed or
     // m = -inf), so the row max is taken only when a sum reaches the limit:
     // on the first tile of a row, or when the scores jump by more than
-    // ~15/c.  Then m moves (to kHeadroom above the row max in the checked
-    // pass) for every row whose max exceeds it, O and l are rescaled, and P
-    // is recomputed (kRescaleP: rescaled).
+    // ~(16 + kHeadroom)/c.  Then m moves (to kHeadroom above the row max in
+    // the checked pass) for every row whose max exceeds it, O and l are
+    // rescaled, and P is recomputed (kRescaleP: rescaled).
     bool rederive = true;
     if (!kSkipFirstExp || t != t_first) {
       if constexpr (OPT) {

@@ -132,7 +132,8 @@ def _scale_keys(k, pattern):
 @pytest.mark.parametrize("dtype", ["fp16", "bf16"])
 def test_score_jumps_vs_oracle(fa, oracle, pattern, causal, dtype):
     """Rows whose scores jump between key tiles: the kernel's exponent offset
-    is re-derived only when a tile's P sum would reach 2^15, which these
+    is re-derived only when a tile's P sum would reach the kernel's limit
+    (61440, below fp16's largest value), which these
     inputs force mid-row, on every tile, in one lane half only, or never
     after the first tile."""
     _note(f"case jumps pattern={pattern} {dtype} causal={causal}")
