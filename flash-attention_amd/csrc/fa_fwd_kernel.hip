@@ -133,6 +133,9 @@ constexpr bool kLdsPoison = false;
 // causal and +1.8 % on causal B2 H16 N4096 with Q, K ~ N(0, 3^2) over 2^15).
 constexpr float kSumLimit = 61440.0f;
 constexpr float kHeadroom = 4.0f;
+static_assert(kSumLimit < 65504.0f, "a P below the sum limit must be finite in fp16");
+static_assert(kHeadroom >= 0.0f && kHeadroom < 14.0f,
+              "the largest P of a re-derived tile, 2^-kHeadroom, must stay a normal fp16");
 
 // The optimistic pass keeps the first key tile's row max as the offset for
 // the whole row; it overflows when a later score exceeds that max by about
