@@ -151,9 +151,11 @@ def test_score_jumps_vs_oracle(fa, oracle, pattern, causal, dtype):
 def test_score_jumps_wide_workgroup_vs_oracle(fa, oracle, pattern, dtype):
     """The same score jumps on the 8-wave workgroup (non-causal, N >= 2048):
     the optimistic pass of fp16 D=128 overflows on "jump", "ramp" and "huge",
-    and the workgroup is recomputed with per-tile checks; bf16 runs only the
-    checked pass.  Its re-derivations rescale the kept fp32 P, except for
-    "huge", where that P is inf and is computed again."""
+    and the workgroup is recomputed with per-tile checks, whose
+    re-derivations rescale the kept fp32 P, except for "huge", where that P
+    is inf and is computed again.  bf16's optimistic pass holds the first
+    tile's offset through "jump" and "ramp" (its P share fp32's range) and
+    overflows, and is redone, only on "huge"."""
     _note(f"case jumps wide pattern={pattern} {dtype}")
     N, D = 2304, 128
     q, k, v = make_qkv(1, 2, N, D, dtype, seed=case_seed(778), device="cpu")
@@ -162,6 +164,24 @@ def test_score_jumps_wide_workgroup_vs_oracle(fa, oracle, pattern, dtype):
     scale = 1.0 / math.sqrt(D)
     o, lse = _fwd(fa, q.to(DEV), k.to(DEV), v.to(DEV), False)
     _check_against_oracle(oracle, q, k, v, o, lse, False, scale, dtype, contract=False)
+
+
+@pytest.mark.parametrize("B,H,N,causal,sigma", [
+    (2, 8, 1000, True, 1.0),    # 4-wave causal
+    (2, 8, 1000, True, 3.0),
+    (1, 2, 2304, False, 1.0),   # 8-wave non-causal
+    (2, 4, 1000, False, 3.0),   # 4-wave non-causal
+])
+def test_bf16_output_same_with_and_without_lse(fa, B, H, N, causal, sigma):
+    """bf16 launches that write an LSE run a second form of the kernel, which
+    keeps the sum of the unrounded p in the optimistic pass; O does not
+    depend on that sum, so it must be bitwise the same either way."""
+    q, k, v = make_qkv(B, H, N, 128, "bf16", seed=case_seed(781), qk_sigma=sigma, device=DEV)
+    o1 = fa.forward(q, k, v, causal=causal)
+    o2, lse = fa.forward(q, k, v, causal=causal, return_lse=True)
+    torch.cuda.synchronize()
+    assert torch.isfinite(lse).all()
+    assert torch.equal(o1, o2)
 
 
 @pytest.mark.parametrize("pattern", ["jump", "half", "ramp", "huge"])

@@ -68,16 +68,19 @@ def test_forward_variants_fit_two_waves_per_simd(device_asm):
     assert len(pair) == 4 and all(args[n][2] == "1" and args[n][3] == "8" and args[n][4] == "0"
                                   for n in pair)
     assert sum("fa_merge_kernel" in n for n, _ in kernels) == 4
-    # the 16x16x32 kernels <D, BF16, CAUSAL, NW>, D = 128: fp16 causal and
-    # non-causal with 4 and 8 waves, bf16 causal with 4, non-causal 4 and 8
-    k16 = {re.search(r"fa_fwd16_kernelILi(\d+)ELb(\d)ELb(\d)ELi(\d)E", n).groups(): f
+    # the 16x16x32 kernels <D, BF16, CAUSAL, NW, LSE_L>, D = 128: fp16 causal
+    # and non-causal with 4 and 8 waves, bf16 causal with 4, non-causal 4 and
+    # 8; bf16 in two forms (with and without the LSE's unrounded sums in the
+    # optimistic pass), fp16 in one
+    k16 = {re.search(r"fa_fwd16_kernelILi(\d+)ELb(\d)ELb(\d)ELi(\d)ELb(\d)E", n).groups(): f
            for n, f in kernels if "fa_fwd16_kernel" in n}
-    assert len(k16) == 7 and all(k[0] == "128" for k in k16), sorted(k16)
-    assert ("128", "1", "1", "8") not in k16, sorted(k16)
-    for (d, bf16, causal, nw), f in k16.items():
+    assert len(k16) == 10 and all(k[0] == "128" for k in k16), sorted(k16)
+    assert not any(k[1] == "1" and k[2] == "1" and k[3] == "8" for k in k16), sorted(k16)
+    assert not any(k[1] == "0" and k[4] == "1" for k in k16), sorted(k16)
+    for (d, bf16, causal, nw, lse_l), f in k16.items():
         # the same 4-tile K/V ring, plus the optimistic pass's flag where it runs
         ring = 4 * 64 * 2 * int(d)
-        opt = bf16 == "0" and (causal == "0" or nw == "8")
+        opt = bf16 == "1" or causal == "0" or nw == "8"
         assert int(f["group_segment_fixed_size"]) == ring + (4 if opt else 0), (d, bf16, causal, nw)
     for name, f in kernels:
         assert int(f["private_segment_fixed_size"]) == 0, (name, "scratch")
