@@ -184,6 +184,45 @@ def test_bf16_output_same_with_and_without_lse(fa, B, H, N, causal, sigma):
     assert torch.equal(o1, o2)
 
 
+@pytest.mark.parametrize("N,jump_tile,causal", [
+    (128, 1, False),    # 4-wave non-causal
+    (128, 1, True),     # 4-wave causal: rows 64..127 see the jump
+    (2048, 5, False),   # 8-wave non-causal
+    (1000, 3, True),
+])
+def test_bf16_large_values_after_a_score_jump(fa, oracle, N, jump_tile, causal):
+    """bf16 keeps the first tile's exponent offset in its optimistic pass, so
+    a key tile whose scores sit ~80 log2 units above the first tile's makes P
+    about 2^80: finite in bf16, and so are the row sums.  With |V| ~ 1e28
+    there, O = sum P * V overflows fp32 although the reference's O (P <= 1)
+    is ~1e28.  The pass must be redone with a checked offset: every element
+    finite and within 1e-2 of the fp64 oracle relative to its row's scale."""
+    D = 128
+    _note(f"case bf16 large values N={N} jump_tile={jump_tile} causal={causal}")
+    gen = torch.Generator().manual_seed(case_seed(782))
+    q = torch.randn(1, 2, N, D, generator=gen) * 0.1
+    k = torch.randn(1, 2, N, D, generator=gen) * 0.1
+    v = torch.randn(1, 2, N, D, generator=gen)
+    q[..., 0] = 25.0                      # score 625 with a jump key: ~80 log2 units
+    k[..., 0] = 0.0
+    jump = slice(64 * jump_tile, 64 * (jump_tile + 1))
+    k[:, :, jump, 0] = 25.0
+    v[:, :, jump, :] = 1e28 * (1.0 + 0.1 * v[:, :, jump, :])
+    q, k, v = (t.to(torch.bfloat16) for t in (q, k, v))
+    scale = 1.0 / math.sqrt(D)
+    # unsplit grid: the 16x16x32 kernel and its optimistic pass
+    o, lse = _fwd(fa, q.to(DEV), k.to(DEV), v.to(DEV), causal, split_kv=False)
+    ref_o, ref_lse = oracle.attn_f64(to_np32(q), to_np32(k), to_np32(v), scale, causal)
+    got = to_np32(o).astype(np.float64)
+    assert np.isfinite(got).all()
+    row_scale = np.maximum(1.0, np.abs(ref_o).max(axis=-1, keepdims=True))
+    rel = float((np.abs(got - ref_o) / row_scale).max())
+    lse_err = float(np.abs(to_np32(lse).astype(np.float64) - ref_lse).max())
+    _note(f"  max rel-to-row err={rel:.3e} lse_err={lse_err:.3e} max|O|={np.abs(ref_o).max():.3e}")
+    assert rel <= 1e-2, rel
+    assert lse_err <= LSE_TOL, lse_err
+
+
 @pytest.mark.parametrize("pattern", ["jump", "half", "ramp", "huge"])
 @pytest.mark.parametrize("causal", [False, True], ids=["noncausal", "causal"])
 @pytest.mark.parametrize("dtype", ["fp16", "bf16"])
