@@ -994,7 +994,7 @@ hipError_t launch_one(const KernelArgs& a, hipStream_t stream) {
 template <int D, bool BF16, bool CAUSAL, int NW>
 hipError_t launch_pick(const KernelArgs& a, hipStream_t stream, bool plain) {
 #ifndef FA_MFMA32
-  if constexpr (D == 128)
+  if constexpr (D == 128 || BF16 || CAUSAL || NW == 8)
     if (plain) return launch16<D, BF16, CAUSAL, NW>(a, stream);
 #endif
   return launch_one<D, BF16, CAUSAL, NW>(a, stream);
@@ -1002,14 +1002,19 @@ hipError_t launch_pick(const KernelArgs& a, hipStream_t stream, bool plain) {
 
 template <int D, bool BF16>
 hipError_t launch_causal(const KernelArgs& a, hipStream_t stream) {
-  // D = 128 launches without split-KV chunks or pair mode (plain order or an
-  // XCD placement table) run fa_fwd16_kernel, the 16x16x32 MFMA form; split
-  // chunks, pair mode and D = 64 run this file's 32x32x16 kernel.  Measured
-  // on two boxes, 16x16x32 against 32x32x16: +2...+8 % at B4 H32 N4096 fp16,
-  // +2...+4 % at bf16 causal B2 H32 N8192, +0...+5 % on fp16 causal
-  // B1 H16 N16384; at D = 64 with 4 waves (B4 H16 N1024) -1...-5 %: there the
-  // softmax's VALU work already matches the MFMA work, and the 16x16 shape
-  // takes twice the MFMA issue slots.  The test-only build
+  // Launches without split-KV chunks or pair mode (plain order or an XCD
+  // placement table) run fa_fwd16_kernel, the 16x16x32 MFMA form, except
+  // fp16 non-causal 4-wave grids at D = 64; split chunks, pair mode and those
+  // run this file's 32x32x16 kernel.  Measured on two boxes, 16x16x32
+  // against 32x32x16: +2...+8 % at B4 H32 N4096 fp16, +2...+4 % at bf16
+  // causal B2 H32 N8192, +0...+5 % on fp16 causal B1 H16 N16384.  At D = 64
+  // (same box): fp16 non-causal 4-wave B4 H16 N1024 -0.3 % (-1.5 % with
+  // Q, K ~ N(0, 3^2)), B3 H16 N1024 -4 %, where the softmax's VALU work
+  // matches the MFMA work and the 16x16 shape takes twice the MFMA issue
+  // slots; but 8-wave B2 H16 N4096 +4.4 % (bf16 +13 %), bf16 B4 H16 N1024
+  // +15 %, causal B2 H16 N4096 +15 % (bf16 +20 %), the causal placement
+  // table B1 H16 N4096 +9 % (bf16 +15 %), causal B1 H16 N16384 with
+  // Q, K ~ N(0, 3^2) +2.7 %.  The test-only build
   // libfa_mi355x_mfma32.so (-DFA_MFMA32) runs the 32x32x16 kernel
   // everywhere, for the counter comparison of the two shapes.
   const bool plain =

@@ -1,5 +1,5 @@
 """GPU parity of both MFMA forms of the fp16 8-wave non-causal kernel: the
-product's 16x16x32 kernel (csrc/fa_fwd_mf16.inc, libfa_mi355x.so) and the
+product's 16x16x32 kernel (csrc/fa_fwd16.inc, libfa_mi355x.so) and the
 32x32x16 form of fa_fwd_kernel (libfa_mi355x_mfma32.so: the kernel source
 compiled with -DFA_MFMA32, same ABI), which exists to compare the two
 shapes by counters (profiles/mfma_shape_16x16_vs_32x32.md); its results must
