@@ -69,9 +69,13 @@ struct KernelArgs {
 };
 
 // Non-causal problems with at least this many keys use 8-wave workgroups;
-// causal fp16 problems from kWideCausalMinSeq keys on.
+// causal fp16 problems from kWideCausalMinSeq keys on, and causal bf16 ones
+// from there when their grid of 128-row q-tiles has fewer than
+// kWideCausalBf16MaxTiles of them (three per four CUs of an MI355X: such
+// grids are split).
 constexpr int kWideMinSeq = 2048;
 constexpr int kWideCausalMinSeq = 8192;
+constexpr int kWideCausalBf16MaxTiles = 192;
 
 // Workgroup rows (BM) of the kernel variant launch_fwd picks for args.
 int block_rows(const KernelArgs& args);

@@ -1020,12 +1020,11 @@ hipError_t launch_causal(const KernelArgs& a, hipStream_t stream) {
   const bool plain =
       a.split.n_items == 0 || (a.split.xcd_heads > 0 && a.split.n_merge == 0);
   if (a.causal) {
-    // Long causal fp16 rows: 8-wave workgroups (+1.4 % at B1 H16 N16384,
-    // +4 % with the matrix-core row sums they enable); bf16 measured neutral
-    // and short problems lose (-11 % at N = 3000: fewer, longer workgroups).
-    if constexpr (!BF16)
-      if (a.seq_len >= kWideCausalMinSeq)
-        return launch_pick<D, BF16, true, 8>(a, stream, plain);
+    // Long causal rows: 8-wave workgroups (fp16: +1.4 % at B1 H16 N16384,
+    // +4 % with the matrix-core row sums they enable; bf16 only where the
+    // 4-wave grid would be split, block_rows); short problems lose (-11 % at N = 3000: fewer,
+    // longer workgroups).
+    if (block_rows(a) == 256) return launch_pick<D, BF16, true, 8>(a, stream, plain);
     // Grids of 0.75 to 2 q-tiles per CU: pair mode (plan_split decides).
     if (a.split.pair) return launch_one<D, BF16, true, 8, true>(a, stream);
     return launch_pick<D, BF16, true, 4>(a, stream, plain);

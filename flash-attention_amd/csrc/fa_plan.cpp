@@ -15,8 +15,16 @@
 namespace fa {
 
 int block_rows(const KernelArgs& a) {
-  // The choice launch_causal makes.
-  if (a.causal) return (!a.bf16 && a.seq_len >= kWideCausalMinSeq) ? 256 : 128;
+  // The choice launch_causal makes.  Causal bf16 takes 8-wave workgroups on
+  // long rows only where the 4-wave grid would be split: same box, against
+  // 4 waves, B1 H2 N8192 +33 % (its split plan); but B1 H4 N8192 D64 (pair
+  // mode) -4.9 %, B1 H8 N8192 (placement table) -2.9 %, B2 H32 N8192 (C4)
+  // -0.7...0 %, and +1...+2 % for B2 H8 N8192 and B1 H16 N16384.
+  if (a.causal) {
+    if (a.seq_len < kWideCausalMinSeq) return 128;
+    const int64_t tiles128 = (int64_t)a.batch * a.heads * ((a.seq_len + 127) / 128);
+    return (!a.bf16 || tiles128 < kWideCausalBf16MaxTiles) ? 256 : 128;
+  }
   return a.seq_len >= kWideMinSeq ? 256 : 128;
 }
 

@@ -63,22 +63,21 @@ def test_forward_variants_fit_two_waves_per_simd(device_asm):
     args = {n: re.search(r"fa_fwd_kernelILi(\d+)ELb(\d)ELb(\d)ELi(\d)ELb(\d)ELb(\d)E", n).groups()
             for n, _ in fwd}
     pair = [n for n, a in args.items() if a[5] == "1"]
-    assert len(fwd) == 32, [n for n, _ in kernels]
+    assert len(fwd) == 36, [n for n, _ in kernels]
     # pair mode: causal, 8 waves, unsplit, D 64/128 x fp16/bf16
     assert len(pair) == 4 and all(args[n][2] == "1" and args[n][3] == "8" and args[n][4] == "0"
                                   for n in pair)
     assert sum("fa_merge_kernel" in n for n, _ in kernels) == 4
     # the 16x16x32 kernels <D, BF16, CAUSAL, NW, LSE_L>, D = 64 and 128: fp16
-    # causal and non-causal with 4 and 8 waves (no fp16 non-causal 4-wave one
-    # at D = 64, which runs the 32x32x16 kernel), bf16 causal with 4,
-    # non-causal 4 and 8; bf16 in two forms (with and without the LSE's
-    # unrounded sums in the optimistic pass), fp16 in one
+    # and bf16, causal and non-causal, with 4 and 8 waves (no fp16 non-causal
+    # 4-wave one at D = 64, which runs the 32x32x16 kernel); bf16 in two
+    # forms (with and without the LSE's unrounded sums in the optimistic
+    # pass), fp16 in one
     k16 = {re.search(r"fa_fwd16_kernelILi(\d+)ELb(\d)ELb(\d)ELi(\d)ELb(\d)E", n).groups(): f
            for n, f in kernels if "fa_fwd16_kernel" in n}
-    assert len(k16) == 19 and {k[0] for k in k16} == {"64", "128"}, sorted(k16)
-    assert sum(k[0] == "128" for k in k16) == 10, sorted(k16)
+    assert len(k16) == 23 and {k[0] for k in k16} == {"64", "128"}, sorted(k16)
+    assert sum(k[0] == "128" for k in k16) == 12, sorted(k16)
     assert not any(k[0] == "64" and k[1:4] == ("0", "0", "4") for k in k16), sorted(k16)
-    assert not any(k[1] == "1" and k[2] == "1" and k[3] == "8" for k in k16), sorted(k16)
     assert not any(k[1] == "0" and k[4] == "1" for k in k16), sorted(k16)
     for (d, bf16, causal, nw, lse_l), f in k16.items():
         # the same 4-tile K/V ring, plus the optimistic pass's flag where it runs
