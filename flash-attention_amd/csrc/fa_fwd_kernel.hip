@@ -157,8 +157,10 @@ constexpr int kVWindow = 4;
 
 
 // SPLIT: the grid runs the work items of args.split (chunks of q-tiles);
-// otherwise one workgroup per q-tile.
-template <int D, bool BF16, bool CAUSAL, int NW, bool SPLIT, bool PAIR = false>
+// otherwise one workgroup per q-tile.  LSE_L (bf16 pair mode and split
+// chunks, launches that write an LSE): the optimistic pass also keeps the
+// sums of the unrounded p, which only the LSE uses.
+template <int D, bool BF16, bool CAUSAL, int NW, bool SPLIT, bool PAIR = false, bool LSE_L = false>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
     fa_fwd_kernel(const KernelArgs args) {
   using T = Tile<D>;
@@ -196,11 +198,21 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
   // sum inf (or NaN), the workgroup votes, and if any row failed it recomputes
   // everything with the per-tile checked pass.  On inputs whose scores never
   // exceed the first tile's max by ~16/c in a row (e.g. the N(0, 1)
-  // benchmark inputs) the second pass never runs.  Pair mode keeps the
+  // benchmark inputs) the second pass never runs.  fp16 pair mode keeps the
   // checked pass: on inputs that fail the spread test (B1 H16 N3000 with
   // Q, K ~ N(0, 3^2)) the optimistic pass and its restart cost 9 %, more
   // than it gains on N(0, 1) inputs (0..+8 %).
-  constexpr bool kMfmaSums = !BF16 && (!CAUSAL || (NW == 8 && !PAIR));
+  // bf16 in pair mode and split chunks runs the optimistic pass too: bf16 P
+  // share fp32's exponent range, so the first tile's offset overflows a P
+  // only ~120 log2 units above that tile's max, where the accumulators turn
+  // inf first; no spread test is needed, and the end-of-pass test also sums
+  // |O| (O can overflow alone when |V| is large).  Same box, against the
+  // checked pass, launches without an LSE (with one): pair mode B1 H16
+  // N3000 +6 % (+1.4 %), with Q, K ~ N(0, 3^2) +12.5 % (+7.4 %), B1 H8
+  // N4096 +6.8 %, B1 H4 N8192 D64 +11 %; split B1 H2 N8192 causal +6.2 %
+  // (+0.9 %), B1 H1 N16384 causal +8.9 %, B1 H2 N4096 +1.8 % (+0.9 %).
+  constexpr bool kMfmaSums = BF16 ? (PAIR || SPLIT) : (!CAUSAL || (NW == 8 && !PAIR));
+  static_assert(!LSE_L || (BF16 && kMfmaSums), "LSE_L: bf16 kernels with an optimistic pass");
   // The first tile of a wave always re-derives the offset (it is -inf), so
   // P is computed only once there, after the row max.  Skipping the first
   // computation measured +0.5…3 % on 4-wave and pair-mode grids, -0.3…0.8 %
@@ -542,13 +554,14 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
           const float p0 = pval(kb, base + 2 * j);
           const float p1 = pval(kb, base + 2 * j + 1);
           w[j] = pack2<BF16>(p0, p1);
-          if constexpr (kUnroundedSum && !OPT) {
+          if constexpr (kUnroundedSum && (!OPT || LSE_L)) {
             // Sum the unrounded fp32 p, as the reference does
             // (online_softmax.cuh:135-152), for the check and the LSE, and
-            // the rounded P for the normalisation.
+            // the rounded P for the normalisation (optimistic pass: the LSE
+            // only; the matrix core sums the rounded P).
             t0 += p0;
             t1 += p1;
-            if constexpr (!kMfmaNorm) tr = dot2_acc<BF16>(w[j], tr);
+            if constexpr (!kMfmaNorm && !OPT) tr = dot2_acc<BF16>(w[j], tr);
           }
         }
         pf[ch] = __builtin_bit_cast(i16x8, w);
@@ -604,7 +617,7 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
       // (In the optimistic pass this is the first tile: O and the sums are
       // still 0, so the rescale below is a no-op for them.)
       const float mx = pair_max(max32(s[0], s[1]));
-      if constexpr (OPT) {
+      if constexpr (OPT && !BF16) {
         // Spread test (kOptSpreadLimit) on the first tile, with the mean
         // estimated from 8 of the row's 64 keys (keys 4g, 4g+9, 4g+50,
         // 4g+59 of each lane half): a wave that fails it asks the workgroup
@@ -652,10 +665,8 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
         pack_pv();
       }
     }
-    if constexpr (!OPT) {
-      l_run += t0 + t1;
-      if constexpr (kUnroundedSum && !kMfmaNorm) lr_run += tr;
-    }
+    if constexpr (!OPT || LSE_L) l_run += t0 + t1;
+    if constexpr (!OPT && kUnroundedSum && !kMfmaNorm) lr_run += tr;
 
     // ---- O^T += V^T P^T ----
     // 4-wave workgroups: raised wave priority while this wave issues its PV
@@ -707,15 +718,26 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
     l_tot = row_sum_of_lane(l_mfma, lane);
     // Vote: did any row of the workgroup overflow (or did the spread test
     // end the pass early)?  The loop ended with a barrier, so every wave is
-    // done with the K/V ring.
-    if (__any(!(l_tot < INFINITY)) && lane == 0) redo_flag = 1;
+    // done with the K/V ring.  bf16: also a sum of |O| that is not finite.
+    bool bad = !(l_tot < INFINITY);
+    if constexpr (BF16) {
+      float sa = 0.0f;
+#pragma unroll
+      for (int db = 0; db < DBLK; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) sa += fabsf(o_acc[db][i]);
+      bad = bad || !(sa < INFINITY);
+    }
+    if (__any(bad) && lane == 0) redo_flag = 1;
     __syncthreads();
     lr_tot = l_tot;
+    if constexpr (LSE_L) l_tot = pair_sum(l_run);
     if (redo_flag != 0) {
 #pragma unroll
       for (int db = 0; db < DBLK; ++db)
 #pragma unroll
         for (int i = 0; i < 16; ++i) o_acc[db][i] = 0.0f;
+      l_mfma = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
       m_run = -INFINITY;
       neg_mc = INFINITY;
       l_run = 0.0f;
@@ -967,15 +989,22 @@ hipError_t launch_one(const KernelArgs& a, hipStream_t stream) {
   // state is neither read nor cleared, so an earlier failure of an unrelated
   // HIP call by the caller is not reported as (or lost to) this launch.
   void* kargs[] = {&args};
-  if (args.split.n_items == 0)
-    return hipLaunchKernel(reinterpret_cast<const void*>(&fa_fwd_kernel<D, BF16, CAUSAL, NW, false, PAIR>),
-                           dim3((unsigned)total), dim3(NW * 64), kargs, 0, stream);
+  // bf16 pair and split launches that write an LSE: the LSE_L form, whose
+  // optimistic pass keeps the unrounded sums.
+  const bool lse_l = BF16 && args.lse != nullptr;
+  if (args.split.n_items == 0) {
+    const void* fn = reinterpret_cast<const void*>(&fa_fwd_kernel<D, BF16, CAUSAL, NW, false, PAIR>);
+    if constexpr (BF16 && PAIR)
+      if (lse_l) fn = reinterpret_cast<const void*>(&fa_fwd_kernel<D, BF16, CAUSAL, NW, false, PAIR, true>);
+    return hipLaunchKernel(fn, dim3((unsigned)total), dim3(NW * 64), kargs, 0, stream);
+  }
   if constexpr (PAIR) {
     return hipErrorInvalidValue;  // (rejected above: pair plans have no items)
   } else {
-    hipError_t e =
-        hipLaunchKernel(reinterpret_cast<const void*>(&fa_fwd_kernel<D, BF16, CAUSAL, NW, true>),
-                        dim3((unsigned)total), dim3(NW * 64), kargs, 0, stream);
+    const void* fn = reinterpret_cast<const void*>(&fa_fwd_kernel<D, BF16, CAUSAL, NW, true>);
+    if constexpr (BF16)
+      if (lse_l) fn = reinterpret_cast<const void*>(&fa_fwd_kernel<D, BF16, CAUSAL, NW, true, false, true>);
+    hipError_t e = hipLaunchKernel(fn, dim3((unsigned)total), dim3(NW * 64), kargs, 0, stream);
     if (e != hipSuccess || sp.n_merge == 0) return e;
     constexpr int RPB = 256 / (D / 4);
     const int64_t merge_blocks = bh * args.split.n_merge * ((BM + RPB - 1) / RPB);

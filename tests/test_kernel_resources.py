@@ -59,14 +59,18 @@ def _kernel_metadata(asm: str):
 def test_forward_variants_fit_two_waves_per_simd(device_asm):
     kernels = _kernel_metadata(device_asm)
     fwd = [(n, f) for n, f in kernels if "fa_fwd_kernel" in n]
-    # template arguments <D, BF16, CAUSAL, NW, SPLIT, PAIR>
-    args = {n: re.search(r"fa_fwd_kernelILi(\d+)ELb(\d)ELb(\d)ELi(\d)ELb(\d)ELb(\d)E", n).groups()
+    # template arguments <D, BF16, CAUSAL, NW, SPLIT, PAIR, LSE_L>
+    args = {n: re.search(r"fa_fwd_kernelILi(\d+)ELb(\d)ELb(\d)ELi(\d)ELb(\d)ELb(\d)ELb(\d)E", n).groups()
             for n, _ in fwd}
     pair = [n for n, a in args.items() if a[5] == "1"]
-    assert len(fwd) == 36, [n for n, _ in kernels]
-    # pair mode: causal, 8 waves, unsplit, D 64/128 x fp16/bf16
-    assert len(pair) == 4 and all(args[n][2] == "1" and args[n][3] == "8" and args[n][4] == "0"
+    assert len(fwd) == 46, [n for n, _ in kernels]
+    # pair mode: causal, 8 waves, unsplit, D 64/128 x fp16/bf16 (bf16 also
+    # in its LSE_L form)
+    assert len(pair) == 6 and all(args[n][2] == "1" and args[n][3] == "8" and args[n][4] == "0"
                                   for n in pair)
+    # LSE_L: only bf16 kernels with an optimistic pass (pair mode, split chunks)
+    lse_l = [a for a in args.values() if a[6] == "1"]
+    assert len(lse_l) == 10 and all(a[1] == "1" and (a[4] == "1" or a[5] == "1") for a in lse_l)
     assert sum("fa_merge_kernel" in n for n, _ in kernels) == 4
     # the 16x16x32 kernels <D, BF16, CAUSAL, NW, LSE_L>, D = 64 and 128: fp16
     # and bf16, causal and non-causal, with 4 and 8 waves (no fp16 non-causal
