@@ -163,24 +163,30 @@ def test_split_c5r_quarter_heads_vs_oracle_and_unsplit(fa, oracle, lib, cus):
     assert lse_err <= LSE_TOL
 
 
-@pytest.mark.parametrize("causal,N,H", [(True, 8192, 2), (False, 4096, 1)],
-                         ids=["causal8192", "noncausal4096"])
-def test_split_wide_workgroup_sampled_rows(fa, oracle, lib, cus, causal, N, H):
+@pytest.mark.parametrize("causal,N,H,dtype,sigma", [
+    (True, 8192, 2, "fp16", 1.0), (False, 4096, 1, "fp16", 1.0),
+    (True, 8192, 2, "bf16", 3.0),   # bf16's optimistic pass on wide scores
+    (False, 4096, 1, "bf16", 3.0),
+], ids=["causal8192", "noncausal4096", "causal8192-bf16-s3", "noncausal4096-bf16-s3"])
+def test_split_wide_workgroup_sampled_rows(fa, oracle, lib, cus, causal, N, H, dtype, sigma):
     """8-wave workgroups (BM = 256) with the optimistic pass, split: sampled
-    rows against the oracle and the reference-kernel emulator."""
-    _note(f"case split wide causal={causal} N={N} H={H}")
+    rows against the oracle and the reference-kernel emulator.  bf16 runs
+    that pass with no spread test, so Q, K ~ N(0, 3^2) keeps the first
+    tile's offset through the rising maxima of a long row."""
+    _note(f"case split wide causal={causal} N={N} H={H} {dtype} sigma={sigma}")
     D = 128
-    q, k, v = make_qkv(1, H, N, D, "fp16", seed=case_seed(903), device=DEV)
+    q, k, v = make_qkv(1, H, N, D, dtype, seed=case_seed(903), qk_sigma=sigma, device=DEV)
     pl = _assert_split(lib, cus, q, k, v, causal)
     assert pl.block_rows == 256
     o, lse, o1, lse1 = _both(fa, q, k, v, causal)
-    _vs_unsplit(o, lse, o1, lse1, "fp16")
+    _vs_unsplit(o, lse, o1, lse1, dtype)
     rng = np.random.default_rng(903)
     heads, sel_bh, sel_row = _sample_rows(N, H, rng, n_random=32)
     qn, kn, vn = to_np32(q), to_np32(k), to_np32(v)
     scale = 1.0 / math.sqrt(D)
     ref_o, ref_lse = oracle.attn_rows_f64(qn, kn, vn, scale, causal, sel_bh, sel_row)
-    emu_o, _ = oracle.kernel_numerics_rows(qn, kn, vn, scale, causal, sel_bh, sel_row, oracle.F16)
+    emu_o, _ = oracle.kernel_numerics_rows(qn, kn, vn, scale, causal, sel_bh, sel_row,
+                                           oracle.BF16 if dtype == "bf16" else oracle.F16)
     got_o = to_np32(o.reshape(H, N, D))[sel_bh, sel_row]
     got_lse = to_np32(lse.reshape(H, N))[sel_bh, sel_row]
     mx, mean = err_stats(got_o, ref_o)
@@ -188,7 +194,9 @@ def test_split_wide_workgroup_sampled_rows(fa, oracle, lib, cus, causal, N, H):
     lse_err = float(np.abs(got_lse.astype(np.float64) - ref_lse).max())
     _note(f"  sampled {len(sel_row)} rows: max_abs={mx:.3e} mean_abs={mean:.3e} "
           f"(ref-kernel emu {emx:.3e}/{emean:.3e}) lse={lse_err:.3e}")
-    assert mx <= MAX_ABS_TOL
+    # bf16 with wide scores: peaked rows put |O| above 1 (the bar scales)
+    o_scale = max(1.0, float(np.abs(ref_o).max())) if dtype == "bf16" else 1.0
+    assert mx <= MAX_ABS_TOL * o_scale
     assert mx <= 2 * emx + 1e-6 and mean <= 2 * emean + 1e-6
     assert lse_err <= LSE_TOL
 
@@ -435,6 +443,7 @@ def _sampled_rows_vs_oracle(oracle, q, k, v, o, lse, dtype, seed, n_random=24):
     (1, 24, 1500, 64, "fp16", 3.0),   # H not a multiple of 8, peaked rows
     (2, 16, 1300, 128, "bf16", 1.0),
     (1, 8, 3000, 128, "fp16", 3.0),   # 192 q-tiles: the lower end of the range
+    (1, 8, 3000, 128, "bf16", 3.0),   # bf16's optimistic pass on wide scores
 ])
 def test_pair_mode_variants_vs_oracle(fa, oracle, lib, cus, B, H, N, D, dtype, sigma):
     """Pair mode at D = 64 and 128, fp16 and bf16, ragged N, several batches:
