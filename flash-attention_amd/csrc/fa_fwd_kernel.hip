@@ -648,12 +648,15 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
       if constexpr (OPT || !kRescaleP) {
         exp_pack(none ? 0.0f : neg_mc);
       } else {
-        // p with the old offset is finite (and within fp32 rounding of the
-        // exact value) while every exponent argument stays below 126; then
-        // the new p is the old one times alpha (<= 1).  Otherwise (the first
-        // tile, m_old = -inf, or a jump of 126 log2 units) p is computed
-        // again from the scores.
-        const bool recompute = !((mx - m_old) * c < 126.0f);
+        // While the offset moves by less than 126 log2 units, p with the old
+        // offset is finite (and within fp32 rounding of the exact value) and
+        // alpha (<= 1) is a normal float, so the new p is the old one times
+        // alpha.  Otherwise (the first tile, m_old = -inf, or a jump of the
+        // scores) p is computed again from the scores: v_exp_f32 flushes a
+        // result below 2^-126 to 0, and the offset sits kHeadroom above the
+        // row max, so testing the max's jump alone would let a jump of
+        // 122...126 units zero the tile that holds the row's new max.
+        const bool recompute = !((m_new - m_old) * c < 126.0f);
         if ((kSkipFirstExp && t == t_first) || __any(recompute)) {
           exp_f32(none ? 0.0f : neg_mc);
         } else {
@@ -718,20 +721,27 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
     l_tot = row_sum_of_lane(l_mfma, lane);
     // Vote: did any row of the workgroup overflow (or did the spread test
     // end the pass early)?  The loop ended with a barrier, so every wave is
-    // done with the K/V ring.  bf16: also a sum of |O| that is not finite.
-    bool bad = !(l_tot < INFINITY);
+    // done with the K/V ring.  bf16: also a sum of |O| that is not finite,
+    // and (LSE_L) the LSE's sum of the unrounded p.  Pair mode adds the two
+    // halves' sums and O after this test, so there each must stay below
+    // 2^126.
+    constexpr float kSumMax = PAIR ? 0x1p126f : INFINITY;
+    bool bad = !(l_tot < kSumMax);
     if constexpr (BF16) {
       float sa = 0.0f;
 #pragma unroll
       for (int db = 0; db < DBLK; ++db)
 #pragma unroll
         for (int i = 0; i < 16; ++i) sa += fabsf(o_acc[db][i]);
-      bad = bad || !(sa < INFINITY);
+      bad = bad || !(sa < kSumMax);
+    }
+    lr_tot = l_tot;
+    if constexpr (LSE_L) {
+      l_tot = pair_sum(l_run);
+      bad = bad || !(l_tot < kSumMax);
     }
     if (__any(bad) && lane == 0) redo_flag = 1;
     __syncthreads();
-    lr_tot = l_tot;
-    if constexpr (LSE_L) l_tot = pair_sum(l_run);
     if (redo_flag != 0) {
 #pragma unroll
       for (int db = 0; db < DBLK; ++db)

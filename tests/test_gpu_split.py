@@ -163,6 +163,60 @@ def test_split_c5r_quarter_heads_vs_oracle_and_unsplit(fa, oracle, lib, cus):
     assert lse_err <= LSE_TOL
 
 
+@pytest.mark.parametrize("B,H,N,D,dtype,causal,kind", [
+    (1, 2, 128, 64, "fp16", True, "plain"),     # 16x16x32 4-wave, checked pass, kept p
+    (1, 2, 128, 64, "fp16", False, "plain"),    # 32x32x16 4-wave D = 64, redone pass
+    (1, 2, 128, 64, "bf16", True, "plain"),     # bf16's optimistic pass redone
+    (1, 2, 128, 64, "bf16", False, "plain"),
+    (1, 2, 2048, 128, "fp16", False, "plain"),  # 8-wave, redone pass, kept p
+    (1, 8, 3000, 128, "fp16", True, "pair"),
+    (1, 8, 3000, 128, "bf16", True, "pair"),
+    (1, 1, 4096, 128, "fp16", False, "split"),
+])
+def test_offset_move_of_128_log2_units(fa, oracle, lib, cus, B, H, N, D, dtype, causal, kind):
+    """Every row's max rises ~128 log2 units on one key tile (a single key).
+    The checked pass moves the offset by that much; where it keeps the tile's
+    fp32 p and rescales them by alpha = 2^-128 instead of computing them
+    again, alpha is below the normal range and exp2 returns 0 for it, which
+    zeroes the tile that holds the row's max (O = 0, LSE = -inf).  Moves of
+    126 log2 units or more must recompute p.  The jump key sits in key tile 1
+    (N = 128) or 2 (the pair-mode halves take alternate tiles, so tile 2 is
+    the second tile of a half)."""
+    _note(f"case offset move 128: {B}x{H}x{N}x{D} {dtype} causal={causal} ({kind})")
+    tdt = torch.float16 if dtype == "fp16" else torch.bfloat16
+    gen = torch.Generator().manual_seed(case_seed(791))
+    q = torch.randn(B, H, N, D, generator=gen) * 0.1
+    k = torch.randn(B, H, N, D, generator=gen) * 0.1
+    v = torch.randn(B, H, N, D, generator=gen)
+    jk = 64 if N == 128 else 128
+    scale = 1.0 / math.sqrt(D)
+    q[..., 0] = 32.0
+    k[..., 0] = 0.0
+    k[:, :, jk, 0] = 128.0 / (32.0 * scale * math.log2(math.e))
+    q, k, v = (t.to(tdt) for t in (q, k, v))
+    rise = 32.0 * float(k[0, 0, jk, 0]) * scale * math.log2(math.e)
+    assert 126.5 < rise < 129.5, rise
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    if kind != "plain":
+        pl = _plan(lib, cus, qd, kd, vd, torch.empty_like(qd), causal)
+        assert ("pair" if pl.key_halves == 2 else "split" if pl.n_items else "other") == kind
+    o, lse = fa.forward(qd, kd, vd, causal=causal, return_lse=True, split_kv=kind != "plain")
+    torch.cuda.synchronize()
+    assert torch.isfinite(o).all().item() and torch.isfinite(lse).all().item()
+    rng = np.random.default_rng(791)
+    _, sel_bh, sel_row = _sample_rows(N, B * H, rng, n_random=32)
+    qn, kn, vn = (to_np32(t.reshape(1, B * H, N, D)) for t in (q, k, v))
+    ref_o, ref_lse = oracle.attn_rows_f64(qn, kn, vn, scale, causal, sel_bh, sel_row)
+    got = to_np32(o.reshape(B * H, N, D))[sel_bh, sel_row].astype(np.float64)
+    got_lse = to_np32(lse.reshape(B * H, N))[sel_bh, sel_row].astype(np.float64)
+    row_scale = np.maximum(1.0, np.abs(ref_o).max(axis=-1, keepdims=True))
+    rel = float((np.abs(got - ref_o) / row_scale).max())
+    lse_err = float(np.abs(got_lse - ref_lse).max())
+    _note(f"  {len(sel_row)} rows: max rel-to-row err={rel:.3e} lse_err={lse_err:.3e}")
+    assert rel <= 1e-2, rel
+    assert lse_err <= LSE_TOL, lse_err
+
+
 @pytest.mark.parametrize("causal,N,H,dtype,sigma", [
     (True, 8192, 2, "fp16", 1.0), (False, 4096, 1, "fp16", 1.0),
     (True, 8192, 2, "bf16", 3.0),   # bf16's optimistic pass on wide scores
