@@ -199,6 +199,53 @@ def test_wide_scores_hand_over_vs_oracle(fa, oracle, B, H, N):
     _check_against_oracle(oracle, q, k, v, o, lse, False, scale, "fp16", contract=False)
 
 
+def test_hand_over_overflow_vote_same_in_every_launch(fa, oracle):
+    """fp16 non-causal 4-wave grids (the 16x16x32 kernel with the first-tile
+    hand-over) whose first tile passes the spread test while a later key's
+    score rises ~120 log2 units, so the optimistic pass overflows and every
+    wave of the workgroup must restart.  The end-of-pass vote must not be
+    taken for a spread-test failure by a wave that reads the flag after a
+    faster wave voted: that wave alone would take the hand-over and the
+    workgroup's barriers would no longer pair up (a whole workgroup's rows
+    non-finite in some launches).  Twelve launches of 376 workgroups: all
+    bitwise equal and finite, sampled rows within the oracle bars."""
+    B, H, N, D = 1, 47, 1024, 128
+    _note(f"case hand-over overflow vote {B}x{H}x{N}x{D}")
+    gen = torch.Generator().manual_seed(case_seed(785))
+    q = torch.randn(B, H, N, D, generator=gen) * 0.5
+    k = torch.randn(B, H, N, D, generator=gen) * 0.5
+    v = torch.randn(B, H, N, D, generator=gen)
+    scale = 1.0 / math.sqrt(D)
+    q[..., 0] = 8.0
+    for j, rise in ((400, 120.0), (940, 90.0)):  # log2 units above the other keys
+        k[:, :, j, :] = 0.0
+        k[:, :, j, 0] = rise * math.log(2) / (8.0 * scale)
+    q, k, v = (t.to(torch.float16) for t in (q, k, v))
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    outs = []
+    for _ in range(12):
+        o, lse = fa.forward(qd, kd, vd, causal=False, return_lse=True, split_kv=False)
+        outs.append((o, lse))
+    torch.cuda.synchronize()
+    o0, lse0 = outs[0]
+    n_bad = [int((~torch.isfinite(o)).any(dim=-1).sum().item()) for o, _ in outs]
+    n_diff = [int((o != o0).any(dim=-1).sum().item()) for o, _ in outs]
+    _note(f"  rows non-finite per launch: {n_bad}; rows differing from launch 0: {n_diff}")
+    assert all(n == 0 for n in n_bad)
+    assert all(torch.equal(o, o0) and torch.equal(lse, lse0) for o, lse in outs)
+    rng = np.random.default_rng(785)
+    _, sel_bh, sel_row = _sample_rows(N, B * H, rng, n_random=24)
+    qn, kn, vn = (to_np32(t.reshape(1, B * H, N, D)) for t in (q, k, v))
+    ref_o, ref_lse = oracle.attn_rows_f64(qn, kn, vn, scale, False, sel_bh, sel_row)
+    got = to_np32(o0.reshape(B * H, N, D))[sel_bh, sel_row]
+    got_lse = to_np32(lse0.reshape(B * H, N))[sel_bh, sel_row].astype(np.float64)
+    mx, _ = err_stats(got, ref_o)
+    lse_err = float(np.abs(got_lse - ref_lse).max())
+    _note(f"  {len(sel_row)} rows: max_abs={mx:.3e} lse_err={lse_err:.3e}")
+    assert mx <= MAX_ABS_TOL
+    assert lse_err <= LSE_TOL
+
+
 @pytest.mark.parametrize("N,jump_tile,causal", [
     (128, 1, False),    # 4-wave non-causal
     (128, 1, True),     # 4-wave causal: rows 64..127 see the jump
