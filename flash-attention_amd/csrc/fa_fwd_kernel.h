@@ -13,9 +13,9 @@ namespace fa {
 // Work plan of a launch, computed on the host (plan_split).
 //
 // Split-KV: long key ranges of a q-tile are cut into chunks computed by
-// separate workgroups, whose partial results (unnormalised fp32 O, offset m
-// and row sum l per row) go to a caller-provided workspace and are merged by
-// a second kernel.  Used when the grid would leave most of the machine idle
+// separate workgroups, whose partial results (fp32 O normalised by the
+// chunk's own row sum, offset m and row sum l per row) go to a
+// caller-provided workspace and are merged by a second kernel.  Used when the grid would leave most of the machine idle
 // behind a few long q-tiles (short causal problems, few heads).
 //
 // XCD placement table (xcd_heads > 0): a causal grid of exactly two q-tiles
@@ -39,10 +39,16 @@ struct SplitPlan {
   // Item i's first partial slot of its q-tile (items of one q-tile use
   // slot[i] + chunk); unused for single-chunk items.  In the XCD placement
   // table: the head (within the XCD's heads) of dispatch position i.
-  uint16_t slot[kMaxSplitItems];
+  // 32-bit like every array here: the kernels read these arrays with scalar
+  // loads at a wave-uniform index, and the compiler may fold a 16-bit
+  // element's byte offset (2i) into the base address of a neighbouring
+  // 32-bit load; scalar loads ignore the base's low two bits, so at odd i
+  // that load returned element i - 1 (item[i] of the XCD placement table
+  // with one head per XCD: every odd q-tile unwritten).
+  uint32_t slot[kMaxSplitItems];
   // Merge list: q-tile (bits 0..15) | chunk count (16..23), first slot in merge_slot.
   uint32_t merge[kMaxSplitItems];
-  uint16_t merge_slot[kMaxSplitItems];
+  uint32_t merge_slot[kMaxSplitItems];
 };
 
 struct KernelArgs {

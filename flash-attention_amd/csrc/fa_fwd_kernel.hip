@@ -722,23 +722,20 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
     // Vote: did any row of the workgroup overflow (or did the spread test
     // end the pass early)?  The loop ended with a barrier, so every wave is
     // done with the K/V ring.  bf16: also a sum of |O| that is not finite,
-    // and (LSE_L) the LSE's sum of the unrounded p.  Pair mode adds the two
-    // halves' sums and O after this test, so there each must stay below
-    // 2^126.
-    constexpr float kSumMax = PAIR ? 0x1p126f : INFINITY;
-    bool bad = !(l_tot < kSumMax);
+    // and (LSE_L) the LSE's sum of the unrounded p.
+    bool bad = !(l_tot < INFINITY);
     if constexpr (BF16) {
       float sa = 0.0f;
 #pragma unroll
       for (int db = 0; db < DBLK; ++db)
 #pragma unroll
         for (int i = 0; i < 16; ++i) sa += fabsf(o_acc[db][i]);
-      bad = bad || !(sa < kSumMax);
+      bad = bad || !(sa < INFINITY);
     }
     lr_tot = l_tot;
     if constexpr (LSE_L) {
       l_tot = pair_sum(l_run);
-      bad = bad || !(l_tot < kSumMax);
+      bad = bad || !(l_tot < INFINITY);
     }
     if (__any(bad) && lane == 0) redo_flag = 1;
     __syncthreads();
@@ -765,10 +762,27 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
     lr_tot = kMfmaNorm ? row_sum_of_lane(l_mfma, lane) : kUnroundedSum ? pair_sum(lr_run) : l_tot;
   }
 
+  // A partial result (a pair half, a split chunk) normalised by its own sum
+  // of the rounded P, that sum's log moved into the offset: m' = m +
+  // log2(lr) / c, O / lr, l / lr, lr' = 1 (m' = -inf, l = 0 where no key was
+  // visible).  Combining partials weights each by exp2((m' - m'_max) c),
+  // which leaves fp32's normal range (v_exp_f32 returns 0 below 2^-126)
+  // only for a partial whose share of the row is that small.  Unnormalised,
+  // bf16's optimistic pass (sums up to 2^127 at the offset of its first
+  // tile, which can lie far below the row max) could lose a partial that
+  // held a significant share.
+  float part_inv = 0.0f;
+  auto normalise_part = [&]() FA_INLINE {
+    part_inv = lr_tot > 0.0f ? 1.0f / lr_tot : 0.0f;
+    m_run = lr_tot > 0.0f ? m_run + __log2f(lr_tot) / c : -INFINITY;
+    l_tot *= part_inv;
+    lr_tot = lr_tot > 0.0f ? 1.0f : 0.0f;
+  };
   if constexpr (PAIR) {
-    // Combine the halves: waves 4-7 hand O (unnormalised), the offset m and
-    // the sums to their row partners through LDS, above the rows the
-    // epilogue stages; each half's terms are rescaled to the larger offset.
+    // Combine the halves: waves 4-7 hand O, the offset m and the sums
+    // (normalised as above) to their row partners through LDS, above the
+    // rows the epilogue stages; each half's terms are rescaled to the
+    // larger offset.
     constexpr int XO = DBLK * 16 * 64;  // floats of O per wave
     static_assert((XO + 4 * 64) * 4 % 1024 == 0 &&
                       256 * D + 4 * (XO + 4 * 64) * 4 <= 8 * T::BYTES,
@@ -790,15 +804,19 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
     __syncthreads();
     if (half == 1) return;
     const f32x4 o1 = *reinterpret_cast<const f32x4*>(xm + 4 * lane);
-    const float m = fmaxf(m_run, o1[0]);
+    const float inv1 = o1[2] > 0.0f ? 1.0f / o1[2] : 0.0f;
+    const float m1 = o1[2] > 0.0f ? o1[0] + __log2f(o1[2]) / c : -INFINITY;
+    normalise_part();
+    const float m = fmaxf(m_run, m1);
     const float a0 = m_run == -INFINITY ? 0.0f : fast_exp2((m_run - m) * c);
-    const float a1 = o1[0] == -INFINITY ? 0.0f : fast_exp2((o1[0] - m) * c);
+    const float a1 = m1 == -INFINITY ? 0.0f : fast_exp2((m1 - m) * c);
+    const float b0 = a0 * part_inv, b1 = a1 * inv1;
 #pragma unroll
     for (int db = 0; db < DBLK; ++db)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) o_acc[db][i] = o_acc[db][i] * a0 + xo[(db * 16 + i) * 64 + lane] * a1;
-    l_tot = l_tot * a0 + o1[1] * a1;
-    lr_tot = lr_tot * a0 + o1[2] * a1;
+      for (int i = 0; i < 16; ++i) o_acc[db][i] = o_acc[db][i] * b0 + xo[(db * 16 + i) * 64 + lane] * b1;
+    l_tot = l_tot * a0 + o1[1] * b1;
+    lr_tot = lr_tot * a0 + (o1[2] > 0.0f ? a1 : 0.0f);
     m_run = m;
   }
   const bool row_ok = qrow < N;
@@ -838,9 +856,11 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
   const int wave_rows = max(0, min(32, N - wrow0));  // rows of this wave below N
 
   if (SPLIT && n_chunks > 1) {
-    // ---- split-KV partial: unnormalised O, offset m (raw score units; -inf
-    // when no key of this chunk is visible to the row), the row sum l for the
-    // LSE and the sum of the rounded P for the normalisation ----
+    // ---- split-KV partial, normalised as above: O, offset m' (raw score
+    // units; -inf when no key of this chunk is visible to the row), the row
+    // sum l for the LSE and the sum of the rounded P (1, or 0 without keys)
+    // for the normalisation ----
+    normalise_part();
     const int64_t slot =
         (int64_t)args.split.slot[item] + chunk;  // (table items are never chunked)
     const int64_t row0 = ((int64_t)bh * args.split.n_slots + slot) * BM + (wrow0 - q0);
@@ -857,8 +877,8 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
 #pragma unroll
               for (int r = 0; r < 4; ++r) {
                 const int db = p * PDB + b;
-                const f32x4 w = {o_acc[db][4 * r + 0], o_acc[db][4 * r + 1], o_acc[db][4 * r + 2],
-                                 o_acc[db][4 * r + 3]};
+                const f32x4 w = f32x4{o_acc[db][4 * r + 0], o_acc[db][4 * r + 1],
+                                      o_acc[db][4 * r + 2], o_acc[db][4 * r + 3]} * part_inv;
                 // cols 32b + 8r + 4g of the pass: chunk 8b + 2r + g
                 put(l32, 8 * b + 2 * r + g, w);
               }
