@@ -85,7 +85,7 @@ size_t plan_chunks(const KernelArgs& a, int compute_units, SplitPlan* plan) {
     slot_base[qb] = n_slots;
     if (nch > 1) {
       plan->merge[n_merge] = (uint32_t)qb | ((uint32_t)nch << 16);
-      plan->merge_slot[n_merge] = (uint16_t)n_slots;
+      plan->merge_slot[n_merge] = (uint32_t)n_slots;
       ++n_merge;
       n_slots += nch;
     }
@@ -102,7 +102,7 @@ size_t plan_chunks(const KernelArgs& a, int compute_units, SplitPlan* plan) {
   for (int i = 0; i < n; ++i) {
     plan->item[i] = (uint32_t)list[i].qb | ((uint32_t)list[i].c << 16) |
                     ((uint32_t)list[i].nch << 24);
-    plan->slot[i] = (uint16_t)(list[i].nch > 1 ? slot_base[list[i].qb] : 0);
+    plan->slot[i] = (uint32_t)(list[i].nch > 1 ? slot_base[list[i].qb] : 0);
   }
   plan->n_items = n;
   plan->n_slots = n_slots;
@@ -149,7 +149,7 @@ size_t plan_xcd_table(const KernelArgs& a, int compute_units, SplitPlan* plan) {
   for (int src = 0; src < cnt; ++src) {
     const int pos = src < alone ? m + src : (src < alone + m ? src - alone : (int)cpx + (cnt - 1 - src));
     plan->item[pos] = (uint32_t)all[src].qb | (1u << 24);
-    plan->slot[pos] = (uint16_t)all[src].head;
+    plan->slot[pos] = (uint32_t)all[src].head;
   }
   plan->n_items = cnt;
   plan->xcd_heads = (int)hpx;
