@@ -110,11 +110,15 @@ using lds::dma_slot;
 // the headroom and another +3.4 % for moving every row, causal B2 H16 N4096
 // with those inputs +3.2 % and +6.4 %, B4 H32 N4096 with them +1.6 % and
 // +2.0 %, C5 +0.7 % and +2.0 %, bf16 causal B2 H32 N8192 with them +0.9 % and
-// +4.2 %.  The cost of the headroom is precision in the smallest p: fp16 p
-// below 2^-14 are subnormal, so keys more than 14 - kHeadroom units under the
-// row max keep fewer bits.  At 4 the score-jump tests stay within 1.25x the
-// emulated reference kernel's error (the bar is 2x); 8 measured 2.05x there
-// and failed.
+// +4.2 % (those gains with a headroom of 4).  The cost of the headroom is
+// precision in the smallest p: fp16 p below 2^-14 are subnormal, so keys more
+// than 14 - kHeadroom units under the row max keep fewer bits.  fp16 takes 1:
+// rows with a few keys 10-30 units above a broad floor of thousands (an
+// attention sink over a long context) measured 4.5x the emulated reference
+// kernel's max-abs error and 6.4x its mean at 4, 2.2x at 2, and 1.0x at 1 and
+// 0 (the bar is 2x); against 4, a headroom of 1 costs C5 1.0 %, C5r 1.9 %
+// and 1.4...3.9 % on other Q, K ~ N(0, 3^2) problems (same box; N(0, 1)
+// inputs unchanged).  bf16 p stay normal down to 2^-126 and keep 4.
 // LDS-poison debug build (compiled with -DFA_LDS_POISON, shipped as
 // libfa_mi355x_poison.so, never the product library): every wave fills the
 // LDS bytes it is about to stage (K/V ring slots, staged Q, the output
@@ -132,10 +136,14 @@ constexpr bool kLdsPoison = false;
 // 15 * 2^12: below fp16's largest finite value, 65504 (+1.3 % on B1 H16 N3000
 // causal and +1.8 % on causal B2 H16 N4096 with Q, K ~ N(0, 3^2) over 2^15).
 constexpr float kSumLimit = 61440.0f;
-constexpr float kHeadroom = 4.0f;
+constexpr float kHeadroomF16 = 1.0f;
+constexpr float kHeadroomBf16 = 4.0f;
+template <bool BF16>
+constexpr float kHeadroom = BF16 ? kHeadroomBf16 : kHeadroomF16;
 static_assert(kSumLimit < 65504.0f, "a P below the sum limit must be finite in fp16");
-static_assert(kHeadroom >= 0.0f && kHeadroom < 14.0f,
+static_assert(kHeadroomF16 >= 0.0f && kHeadroomF16 < 14.0f,
               "the largest P of a re-derived tile, 2^-kHeadroom, must stay a normal fp16");
+static_assert(kHeadroomBf16 >= 0.0f && kHeadroomBf16 < 100.0f, "bf16 P must stay normal");
 
 // The optimistic pass keeps the first key tile's row max as the offset for
 // the whole row; it overflows when a later score exceeds that max by about
@@ -629,7 +637,7 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
       }
       const float m_old = m_run;
       const bool grow = mx > m_run;  // false when both are -inf
-      const float m_new = grow ? (OPT ? mx : mx + kHeadroom / c) : m_run;
+      const float m_new = grow ? (OPT ? mx : mx + kHeadroom<BF16> / c) : m_run;
       // exp2(0) = 1 for rows that keep their offset (branch-free: also
       // covers m_run = -inf, where m_run - m_new would be NaN).
       const float alpha = fast_exp2(grow ? (m_run - m_new) * c : 0.0f);

@@ -246,6 +246,45 @@ def test_hand_over_overflow_vote_same_in_every_launch(fa, oracle):
     assert lse_err <= LSE_TOL
 
 
+@pytest.mark.parametrize("split_kv", [False, True], ids=["unsplit", "split"])
+@pytest.mark.parametrize("N,rise", [(16384, 18.0), (8192, 15.0)])
+def test_fp16_sink_over_a_long_row(fa, oracle, N, rise, split_kv):
+    """fp16 rows with one key (an attention sink) `rise` log2 units above a
+    floor of N - 1 keys: the first tile fails the optimistic pass's spread
+    test, and the checked pass puts its offset kHeadroom above the row max,
+    so the floor's P (2^-(rise + kHeadroom)) are subnormal in fp16 and keep
+    fewer bits than the reference kernel's (P <= 1).  Their sum is a large
+    share of the row; the error must stay within 2x the emulated reference
+    kernel's (a headroom of 4 measured 4.3x here)."""
+    B, H, D = 1, 2, 64
+    _note(f"case fp16 sink N={N} rise={rise} split_kv={split_kv}")
+    gen = torch.Generator().manual_seed(case_seed(787))
+    q = torch.randn(B, H, N, D, generator=gen) * 0.1
+    k = torch.randn(B, H, N, D, generator=gen) * 0.1
+    v = torch.randn(B, H, N, D, generator=gen)
+    scale = 1.0 / math.sqrt(D)
+    q[..., 0] = 8.0
+    k[..., 0] = 0.0
+    k[:, :, 0, 0] = rise * math.log(2) / (8.0 * scale)
+    q, k, v = (t.to(torch.float16) for t in (q, k, v))
+    o, lse = _fwd(fa, q.to(DEV), k.to(DEV), v.to(DEV), False, split_kv=split_kv)
+    rng = np.random.default_rng(787)
+    _, sel_bh, sel_row = _sample_rows(N, B * H, rng, n_random=48)
+    qn, kn, vn = (to_np32(t.reshape(1, B * H, N, D)) for t in (q, k, v))
+    ref_o, ref_lse = oracle.attn_rows_f64(qn, kn, vn, scale, False, sel_bh, sel_row)
+    emu_o, _ = oracle.kernel_numerics_rows(qn, kn, vn, scale, False, sel_bh, sel_row, oracle.F16)
+    got = to_np32(o.reshape(B * H, N, D))[sel_bh, sel_row]
+    got_lse = to_np32(lse.reshape(B * H, N))[sel_bh, sel_row].astype(np.float64)
+    mx, mean = err_stats(got, ref_o)
+    emx, emean = err_stats(emu_o, ref_o)
+    lse_err = float(np.abs(got_lse - ref_lse).max())
+    _note(f"  {len(sel_row)} rows: max_abs={mx:.3e} mean_abs={mean:.3e} "
+          f"(ref-kernel emu {emx:.3e}/{emean:.3e}) lse={lse_err:.3e}")
+    assert mx <= MAX_ABS_TOL and mean <= MEAN_ABS_TOL
+    assert mx <= 2 * emx + 1e-6 and mean <= 2 * emean + 1e-6
+    assert lse_err <= LSE_TOL
+
+
 @pytest.mark.parametrize("N,jump_tile,causal", [
     (128, 1, False),    # 4-wave non-causal
     (128, 1, True),     # 4-wave causal: rows 64..127 see the jump
