@@ -246,6 +246,45 @@ def test_hand_over_overflow_vote_same_in_every_launch(fa, oracle):
     assert lse_err <= LSE_TOL
 
 
+@pytest.mark.parametrize("B,H,N,D,dtype,causal", [
+    (16, 64, 16384, 128, "fp16", True),     # 4 GiB per tensor: byte offsets past 2^32
+    (2, 2, 1 << 20, 128, "bf16", True),     # a 2^20-row sequence
+])
+def test_huge_problem_sampled_rows(fa, oracle, B, H, N, D, dtype, causal):
+    """Problems far larger than the BASELINE ones (MI355X holds 288 GB):
+    rows of the first, a middle and the last head against the fp64 oracle and
+    the emulated reference kernel, so that no offset (batch, head, row) is
+    computed in 32 bits where it can exceed them."""
+    _note(f"case huge {B}x{H}x{N}x{D} {dtype} causal={causal}")
+    g = torch.Generator(device=DEV)
+    g.manual_seed(case_seed(789))
+    tdt = torch.float16 if dtype == "fp16" else torch.bfloat16
+    q, k, v = (torch.randn(B, H, N, D, generator=g, device=DEV, dtype=torch.float32).to(tdt)
+               for _ in range(3))
+    o, lse = _fwd(fa, q, k, v, causal)
+    scale = 1.0 / math.sqrt(D)
+    for b, h in ((0, 0), (B // 2, H // 3), (B - 1, H - 1)):
+        rows = np.unique(np.array([0, 1, N // 2, N - 2, N - 1]
+                                  + np.random.default_rng(b + h).integers(0, N, 8).tolist(),
+                                  np.int32))
+        qn, kn, vn = (to_np32(t[b, h])[None, None] for t in (q, k, v))
+        sel_bh = np.zeros(len(rows), np.int32)
+        ref_o, ref_lse = oracle.attn_rows_f64(qn, kn, vn, scale, causal, sel_bh, rows)
+        emu_o, _ = oracle.kernel_numerics_rows(qn, kn, vn, scale, causal, sel_bh, rows,
+                                               oracle.BF16 if dtype == "bf16" else oracle.F16)
+        got = to_np32(o[b, h])[rows]
+        got_lse = to_np32(lse[b, h])[rows].astype(np.float64)
+        mx, mean = err_stats(got, ref_o)
+        emx, emean = err_stats(emu_o, ref_o)
+        lse_err = float(np.abs(got_lse - ref_lse).max())
+        _note(f"  b={b} h={h}: max_abs={mx:.3e} mean_abs={mean:.3e} "
+              f"(ref-kernel emu {emx:.3e}/{emean:.3e}) lse={lse_err:.3e}")
+        assert np.isfinite(got).all()
+        assert mx <= MAX_ABS_TOL and mean <= MEAN_ABS_TOL
+        assert mx <= 2 * emx + 1e-6 and mean <= 2 * emean + 1e-6
+        assert lse_err <= LSE_TOL
+
+
 @pytest.mark.parametrize("split_kv", [False, True], ids=["unsplit", "split"])
 @pytest.mark.parametrize("N,rise", [(16384, 18.0), (8192, 15.0)])
 def test_fp16_sink_over_a_long_row(fa, oracle, N, rise, split_kv):
