@@ -662,8 +662,9 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
         // alpha.  Otherwise (the first tile, m_old = -inf, or a jump of the
         // scores) p is computed again from the scores: v_exp_f32 flushes a
         // result below 2^-126 to 0, and the offset sits kHeadroom above the
-        // row max, so testing the max's jump alone would let a jump of
-        // 122...126 units zero the tile that holds the row's new max.
+        // row max, so testing the max's jump alone would let a jump within
+        // kHeadroom below 126 units zero the tile that holds the row's new
+        // max.
         const bool recompute = !((m_new - m_old) * c < 126.0f);
         if ((kSkipFirstExp && t == t_first) || __any(recompute)) {
           exp_f32(none ? 0.0f : neg_mc);
